@@ -1,0 +1,355 @@
+"""Benchmark of one decode-attention layer call of the top-k sparse path on one MI355X.
+
+A step is one layer call: block selection (scorer + top-k, one launch) followed by the
+sparse paged finalize (one launch, fused split-K merge).  The default workload is
+batch 16, 131072-token contexts, 32 query / 8 KV heads, head_dim
+128, KV block 128, top-64 blocks per KV head, bf16 K/V in a paged pool of 16-token
+pages in randomly permuted order, bf16 k_bar summaries.  Inputs are synthetic
+(q, K, V ~ N(0,1)), resident in HBM before timing starts.  ``--layers`` independent
+pools are rotated through so consecutive calls never re-read the same K/V pages
+(the 256 MB MALL cannot hold the per-call working set).
+
+Prints one JSON line (see the keys below).  ``--gpus`` above 1 is rejected: this
+build runs on one GPU.
+"""
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import interattn_amd as ia  # noqa: E402
+
+HBM_PEAK_GBPS = 8000.0
+
+WORKLOADS = {
+    # name: batch, hq, hkv, d, seq_len (or "c3"), page, block, k, forced_first, forced_last, kv dtype
+    "c4": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="bf16"),
+    "c5": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="fp8"),
+    "c2": dict(batch=1, hq=32, hkv=8, d=128, seq=32768, page=16, block=64, k=64, ff=1, fl=2, kv="bf16"),
+    "c3": dict(batch=16, hq=32, hkv=8, d=128, seq="c3", page=16, block=64, k=None, ff=0, fl=0, kv="bf16"),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of hipGraph replay")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-seqs", type=int, default=2)
+    return ap.parse_args()
+
+
+def c3_lengths():
+    import numpy as np
+
+    rng = np.random.default_rng(1236)
+    return [int(x) for x in rng.integers(8192, 65537, size=16)]
+
+
+def make_layer(w, dev, gen, lens, table, n_pages):
+    hkv, page, d = w["hkv"], w["page"], w["d"]
+    shape = (n_pages, hkv, page, d)
+    if w["kv"] == "fp8":
+        pk = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
+        pv = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
+        ks = (pk.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
+        vs = (pv.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
+        pool_k = (pk.float() / ks[:, :, None, None]).to(torch.float8_e4m3fn)
+        pool_v = (pv.float() / vs[:, :, None, None]).to(torch.float8_e4m3fn)
+        del pk, pv
+        scales = (ks, vs)
+    else:
+        pool_k = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
+        pool_v = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
+        scales = None
+    q = torch.randn((w["batch"], w["hq"], d), device=dev, dtype=torch.bfloat16, generator=gen)
+    seq_lens = torch.tensor(lens, device=dev, dtype=torch.int32)
+    nb_max = max(math.ceil(L / w["block"]) for L in lens)
+    summ = ia.build_block_summaries(pool_k, pool_v, table, seq_lens, w["block"], nb_max=nb_max,
+                                    k_bar_dtype=torch.bfloat16, scales=scales)
+    return dict(pool_k=pool_k, pool_v=pool_v, scales=scales, q=q, seq_lens=seq_lens, k_bar=summ["k_bar"],
+                ws={}, out=torch.empty_like(q))
+
+
+def layer_call(L, w, table, kvec, k_cap):
+    idx, n_sel = ia.select_blocks_topk(L["q"], L["k_bar"], L["seq_lens"], w["k"] or 0, block_size=w["block"],
+                                       forced_first=w["ff"], forced_last=w["fl"], k_per_seq=kvec, k_cap=k_cap,
+                                       workspace=L["ws"])
+    ia.sparse_paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], idx, n_sel,
+                           block_size=w["block"], scales=L["scales"], out=L["out"], workspace=L["ws"])
+    return idx, n_sel
+
+
+def algorithmic_bytes(w, lens, n_sel_list):
+    """Compulsory bytes of one layer call: q + out, the k_bar rows the scorer reads,
+    the selected blocks' valid K+V tokens, and fp8 scales of the touched pages."""
+    d, hq, hkv, block, page = w["d"], w["hq"], w["hkv"], w["block"], w["page"]
+    s_kv = 1 if w["kv"] == "fp8" else 2
+    qo = 2 * hq * d * 2 * len(lens)
+    summ = sum(hkv * math.ceil(L / block) * d * 2 for L in lens)
+    kv = 0
+    scales = 0
+    for b, L in enumerate(lens):
+        for h in range(hkv):
+            for j in n_sel_list[b][h]:
+                toks = min(block, L - j * block)
+                kv += toks * d * 2 * s_kv
+                if w["kv"] == "fp8":
+                    scales += math.ceil(toks / page) * 2 * 4
+    return qo, summ, kv + scales
+
+
+def time_events(fn, n, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(n):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n
+
+
+def cpu_baseline(w, L0, table, lens, idx_host, nsel_host, n_seqs):
+    """The oracle (numpy restatement of the reference's CPU path) on a bounded sample:
+    ``n_seqs`` sequences of layer 0, all KV heads: top-k scores from the cached k_bar
+    summaries, selection, then attention over the gathered selected tokens.  Returns
+    microseconds per full layer call (scaled by batch / n_seqs)."""
+    import numpy as np
+
+    from oracle import attention as A
+    from oracle import select as S
+
+    d, hq, hkv, block, page = w["d"], w["hq"], w["hkv"], w["block"], w["page"]
+    g = hq // hkv
+    pool_k = L0["pool_k"]
+    pool_v = L0["pool_v"]
+    inputs = []
+    for b in range(n_seqs):
+        nb = math.ceil(lens[b] / block)
+        kb = L0["k_bar"][b, :, :nb].float().cpu().numpy()
+        q = L0["q"][b].float().cpu().numpy()
+        kv_blocks = {}
+        for h in range(hkv):
+            for j in idx_host[b][h][:nsel_host[b][h]]:
+                pages = table[b, j * block // page:(j * block + block) // page].long()
+                kv_blocks[(h, int(j))] = (pool_k[pages, h].float().reshape(-1, d).cpu().numpy(),
+                                          pool_v[pages, h].float().reshape(-1, d).cpu().numpy())
+        inputs.append((q, kb, nb, kv_blocks))
+    counts_full = None
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for q, kb, nb, kv_blocks in inputs:
+            counts = np.full(nb, block)
+            sc = S.topk_block_scores(q, kb, counts, g)
+            for h in range(hkv):
+                sel = S.select_topk(sc[h], nb, w["k"] or max(16, nb // 16), w["ff"], w["fl"], False)
+                ks = np.concatenate([kv_blocks[(h, int(j))][0] for j in sel if (h, int(j)) in kv_blocks] or
+                                    [np.zeros((0, d))])
+                vs = np.concatenate([kv_blocks[(h, int(j))][1] for j in sel if (h, int(j)) in kv_blocks] or
+                                    [np.zeros((0, d))])
+                A.dense_decode(q[h * g:(h + 1) * g], ks[None], vs[None])
+        reps += 1
+        if time.perf_counter() - t0 > 10.0 or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    del counts_full
+    return dt / n_seqs * len(lens) * 1e6, reps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        sys.exit(2)
+    w = dict(WORKLOADS[args.workload])
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lens = c3_lengths() if w["seq"] == "c3" else [w["seq"]] * w["batch"]
+    w["batch"] = len(lens)
+    pages_per = [math.ceil(L / w["page"]) for L in lens]
+    n_pages = sum(pages_per)
+    max_pages = max(pages_per)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1237)
+    perm = torch.randperm(n_pages, device=dev, generator=gen).to(torch.int32)
+    table = torch.full((len(lens), max_pages), -1, device=dev, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(pages_per):
+        table[b, :n] = perm[off:off + n]
+        off += n
+    kvec = None
+    k_cap = None
+    if w["k"] is None:     # C3: k_i = max(16, nb_i // 16)
+        ks = [max(16, math.ceil(L / w["block"]) // 16) for L in lens]
+        kvec = torch.tensor(ks, device=dev, dtype=torch.int32)
+        k_cap = max(ks) + w["ff"] + w["fl"]
+    t_setup = time.perf_counter()
+    layers = [make_layer(w, dev, gen, lens, table, n_pages) for _ in range(args.layers)]
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] workload={args.workload} layers={args.layers} setup {setup_s:.1f}s", file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream()
+    # selection results of layer 0 (for byte accounting and the CPU baseline)
+    idx0, nsel0 = layer_call(layers[0], w, table, kvec, k_cap)
+    torch.cuda.synchronize()
+    idx_h = idx0.cpu().numpy()
+    nsel_h = nsel0.cpu().numpy()
+    sel_lists = [[idx_h[b, h, :nsel_h[b, h]] for h in range(w["hkv"])] for b in range(len(lens))]
+    qo_b, summ_b, kv_b = algorithmic_bytes(w, lens, sel_lists)
+    total_bytes = qo_b + summ_b + kv_b
+
+    # warmup (also builds every workspace before capture)
+    for i in range(args.warmup):
+        for L in layers:
+            layer_call(L, w, table, kvec, k_cap)
+    torch.cuda.synchronize()
+
+    use_graph = not args.no_graph
+    graph = None
+    if use_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for L in layers:
+                layer_call(L, w, table, kvec, k_cap)
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        # the captured graph must reproduce the eager outputs
+        ref = [L["out"].clone() for L in layers]
+        for L in layers:
+            L["out"].zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for L, r in zip(layers, ref):
+            layer_call(L, w, table, kvec, k_cap)
+        torch.cuda.synchronize()
+        graph_ok = all(torch.equal(L["out"], r) for L, r in zip(layers, ref))
+        if not graph_ok:
+            print("[bench] graph replay mismatch; timing eager launches", file=sys.stderr, flush=True)
+            use_graph = False
+
+    nl = len(layers)
+    replays = max(1, args.steps // nl)
+    steps = replays * nl
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    if use_graph:
+        for _ in range(replays):
+            graph.replay()
+    else:
+        for _ in range(replays):
+            for L in layers:
+                layer_call(L, w, table, kvec, k_cap)
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = start.elapsed_time(end)
+    us_per_layer = ms_total * 1e3 / steps
+
+    # per-kernel averages (eager back-to-back launches on this stream)
+    idxs = [layer_call(L, w, table, kvec, k_cap) for L in layers]
+    torch.cuda.synchronize()
+    nrep = max(8, args.steps // (2 * nl))
+
+    def run_select():
+        for L in layers:
+            ia.select_blocks_topk(L["q"], L["k_bar"], L["seq_lens"], w["k"] or 0, block_size=w["block"],
+                                  forced_first=w["ff"], forced_last=w["fl"], k_per_seq=kvec, k_cap=k_cap,
+                                  workspace=L["ws"])
+
+    def run_finalize():
+        for L, (ix, ns) in zip(layers, idxs):
+            ia.sparse_paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], ix, ns,
+                                   block_size=w["block"], scales=L["scales"], out=L["out"], workspace=L["ws"])
+
+    sel_us = time_events(run_select, nrep, stream) * 1e3 / nl
+    fin_us = time_events(run_finalize, nrep, stream) * 1e3 / nl
+    fin_bytes = qo_b + kv_b
+    fin_gbps = fin_bytes / (fin_us * 1e-6) / 1e9
+
+    dense_us = None
+    if not args.no_dense:
+        L = layers[0]
+        ia.paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], max_seq_len=max(lens),
+                        scales=L["scales"], out=L["out"], workspace=L["ws"])
+        torch.cuda.synchronize()
+
+        def run_dense():
+            for L in layers:
+                ia.paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], max_seq_len=max(lens),
+                                scales=L["scales"], out=L["out"], workspace=L["ws"])
+
+        dense_us = time_events(run_dense, 3, stream) * 1e3 / nl
+
+    s_kv = 1 if w["kv"] == "fp8" else 2
+    dense_bytes = qo_b + sum(w["hkv"] * L * w["d"] * 2 * s_kv for L in lens)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        n_s = min(args.cpu_sample_seqs, len(lens))
+        cpu_us, reps = cpu_baseline(w, layers[0], table, lens, idx_h, nsel_h, n_s)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
+               "sample": f"{n_s} of {len(lens)} sequences of one layer call, all {w['hkv']} KV heads "
+                         f"(numpy oracle: scores from cached k_bar, top-k, attention over gathered selected "
+                         f"tokens), {reps} reps, scaled by {len(lens)}/{n_s}",
+               "cpu": platform.processor() or platform.machine()}
+
+    dtype = "fp8e4m3-kv/bf16-q" if w["kv"] == "fp8" else "bf16"
+    line = {
+        "metric": "\u00b5s per decode-attn layer + achieved HBM GB/s (% peak), 32K\u2013128K ctx",
+        "value": round(us_per_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_layer / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic N(0,1) q/K/V, random page permutation, seed 1237",
+        "config": {"workload": f"BASELINE config {args.workload[1:]}", "batch": len(lens),
+                   "seq_len": lens[0] if len(set(lens)) == 1 else f"ragged {min(lens)}..{max(lens)}",
+                   "q_heads": w["hq"], "kv_heads": w["hkv"], "head_dim": w["d"], "kv_block": w["block"],
+                   "page": w["page"], "top_k": w["k"] if w["k"] else "max(16, nb/16)",
+                   "forced_first": w["ff"], "forced_last": w["fl"], "layers_rotated": nl,
+                   "launch": "hipgraph" if use_graph else "eager"},
+        "achieved_GBps": round(total_bytes / (us_per_layer * 1e-6) / 1e9, 1),
+        "pct_hbm_peak": round(100 * total_bytes / (us_per_layer * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes": {"total": total_bytes, "q_out": qo_b, "k_bar": summ_b, "selected_kv": kv_b},
+        "kernels_us": {"select_topk": round(sel_us, 3), "paged_finalize": round(fin_us, 3)},
+        "roofline": {"bound": "hbm", "kernel": "ia_condition_block_paged_finalize", "achieved": round(fin_gbps, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(fin_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": None},
+        "dense_us": None if dense_us is None else round(dense_us, 2),
+        "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
+        "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us_per_layer, 2),
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,174 @@
+/*
+ * interattn_amd -- C ABI of the MI355X (gfx950) condition-block sparse
+ * decode-attention library.
+ *
+ * Every entry point takes plain device pointers, sizes and strides, launches
+ * asynchronously on the given HIP stream (NULL = the default stream), never
+ * allocates device memory, never synchronises, and returns 0 on success or a
+ * non-zero IA_ERR_* code.  ia_last_error() returns the message of the last
+ * failure on the calling thread.  Scratch memory comes from a caller-owned
+ * workspace whose size is given by the matching *_workspace_size() function;
+ * the workspace must be zero-filled once before its first use, and every entry
+ * point leaves its counters zeroed again for the next call.  Calls that share
+ * one workspace must not overlap.
+ *
+ * Reference paths below are relative to the reference repository root;
+ * CBT = llama/script/analysis/condition_block_gen/methods/condition_block_triton_impl,
+ * CBG = llama/script/analysis/condition_block_gen.
+ */
+#ifndef INTERATTN_AMD_H
+#define INTERATTN_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define IA_API __attribute__((visibility("default")))
+#else
+#define IA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. */
+enum {
+  IA_F32 = 0,
+  IA_BF16 = 1,
+  IA_FP8_E4M3 = 2, /* OCP e4m3fn, dequantised as code * scale[page, kv_head] */
+};
+
+/* Error codes. */
+enum {
+  IA_OK = 0,
+  IA_ERR_INVALID = 1,     /* argument outside the supported contract */
+  IA_ERR_UNSUPPORTED = 2, /* valid combination with no kernel instance */
+  IA_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  IA_ERR_LAUNCH = 4,      /* HIP reported a launch error */
+};
+
+/*
+ * A paged K/V source.  Row (token) t of page p for kv head h starts at
+ *   k + (p * k_page_stride + h * k_head_stride + t * k_token_stride) elements
+ * and holds head_dim contiguous elements; the same for v.  Logical token i of
+ * batch entry b lives in page block_table[b * bt_stride + i / page_size] at row
+ * i % page_size (only the first bt_cols entries of a row are ever read).
+ * block_table == NULL means the identity table (page = i /
+ * page_size), which describes the reference's contiguous padded prompt view
+ * [Hkv, nb, B, D] (CBT/core.py:383-408) with page_size = B.  Page ids outside
+ * [0, n_pages) are skipped (they contribute nothing) instead of being read.
+ * For IA_FP8_E4M3, k_scale/v_scale hold one float per (page, kv head) at
+ * scale[p * scale_page_stride + h].
+ */
+typedef struct ia_paged_kv {
+  const void* k;
+  const void* v;
+  int32_t dtype;
+  int32_t page_size; /* tokens per page; a multiple of 16 */
+  int64_t n_pages;
+  int64_t k_page_stride, k_head_stride, k_token_stride;
+  int64_t v_page_stride, v_head_stride, v_token_stride;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  int64_t bt_cols; /* valid entries per block-table row; pages past it are skipped */
+  const float* k_scale;
+  const float* v_scale;
+  int64_t scale_page_stride;
+} ia_paged_kv;
+
+/* Query / output geometry: q[b, row, :] at q + b * q_batch_stride + row * q_row_stride,
+ * rows = n_q_heads, row h*G+g attends kv head h (G = n_q_heads / n_kv_heads). */
+typedef struct ia_decode_shape {
+  int32_t batch;
+  int32_t n_q_heads;
+  int32_t n_kv_heads;
+  int32_t head_dim; /* 64 or 128 */
+  int64_t q_batch_stride;
+  int64_t q_row_stride;
+  int32_t q_dtype; /* IA_F32 or IA_BF16 */
+} ia_decode_shape;
+
+IA_API const char* ia_last_error(void);
+IA_API int ia_version(void);
+
+/*
+ * Per-block summaries of a paged sequence batch: over the valid tokens of each
+ * logical block of block_size tokens, counts, mean key k_bar, mean value
+ * v_bar, elementwise k_max / k_min and the max token value-norm v_norm_max,
+ * plus v_norm_all = max over blocks.  Replaces _build_prompt_blocks
+ * (CBT/core.py:449-500) for paged pools.  Outputs are [batch, Hkv, nb_max, D]
+ * (k_bar, v_bar, k_max, k_min), [batch, Hkv, nb_max] (v_norm_max),
+ * [batch, Hkv] (v_norm_all) and [batch, nb_max] (counts, int32); any output
+ * pointer except counts may be NULL to skip it.  Blocks at or past a
+ * sequence's end get count 0, zero means and -inf/+inf/-inf extrema/norms.
+ * seq_lens is a device array [batch].
+ */
+IA_API int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* seq_lens, int32_t batch,
+                             int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                             int32_t nb_max, void* k_bar, int32_t k_bar_dtype, void* v_bar,
+                             int32_t v_bar_dtype, void* k_max, void* k_min,
+                             int32_t bounds_dtype, float* v_norm_max, float* v_norm_all,
+                             int32_t* counts, void* stream);
+
+/*
+ * Top-k block selection.  score[b,h,j] = mean_g(q[b,h*G+g] . k_bar[b,h,j]) / sqrt(D)
+ * (group-mean representative score of CBG/methods/quest.py:91-103 with the mean
+ * key as representative).  Per (b, h) the result is the forced blocks (the
+ * first forced_first and last forced_last valid blocks) plus the top k_eff of
+ * the others by score, ties to the lower index, with k_eff = k - #forced when
+ * forced_in_k else k (k_per_seq, a device array [batch], overrides k per
+ * sequence when non-NULL).  idx[b, h, 0:n_sel[b,h]] receives the chosen block ids in
+ * ascending order (idx row stride k_cap >= k_eff + #forced).  scores may be
+ * NULL; otherwise it receives [batch, Hkv, nb_max] float32 (-inf past the end).
+ * k_bar: [batch, Hkv, nb_max, D] of k_bar_dtype (IA_F32 or IA_BF16) at
+ * (b * kbar_batch_stride + h * kbar_head_stride + j * D).
+ * New entry point: the reference selects by an eps threshold only
+ * (_select_prompt_blocks_triton, CBT/core.py:701-744).
+ */
+IA_API size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t nb_max);
+IA_API int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_bar,
+                   int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
+                   const int32_t* seq_lens, int32_t block_size, int32_t nb_max, int32_t k,
+                   const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last,
+                   int32_t forced_in_k,
+                   int32_t* idx, int32_t k_cap, int32_t* n_sel, float* scores, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/*
+ * Sparse paged decode (finalize attention over selected blocks).  For each
+ * (b, q row) the softmax of q . K^T * scale over the valid tokens of the blocks
+ * idx[b, h, 0:n_sel[b,h]] (block_size tokens each), applied to V; split-K over
+ * chunks of blocks with an online-softmax merge (CBT/page_attention.py:206-255,
+ * CBT/legacy.py:765-794).  out: [batch, n_q_heads, D] contiguous, out_dtype
+ * IA_F32 or IA_BF16.  Replaces the selected-page stream of
+ * _condition_block_finalize_attention_kernel for the top-k rule.
+ */
+IA_API size_t ia_paged_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
+                                      int32_t head_dim, int32_t max_items);
+IA_API int ia_sparse_paged_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
+                           const int32_t* seq_lens, int32_t block_size, const int32_t* idx,
+                           int32_t k_cap, const int32_t* n_sel, float scale, void* out,
+                           int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/*
+ * Dense paged decode: softmax(q . K^T * scale) V over every valid token
+ * (seq_lens[b] tokens) of each sequence.  The dense fallback of
+ * _sdpa_full_attention_forward (CBT/core.py:1158-1177) over a paged pool.
+ */
+IA_API int ia_paged_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
+                    const int32_t* seq_lens, int32_t max_seq_len, float scale, void* out,
+                    int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Number of split-K items per (b, h) the two decode entry points use for the
+ * given workload; size the decode workspace with it.  max_seq_len must bound
+ * every seq_lens[b] passed to ia_paged_decode (tokens past it are not read). */
+IA_API int32_t ia_sparse_max_items(int32_t batch, int32_t n_kv_heads, int32_t k_cap);
+IA_API int32_t ia_dense_max_items(int32_t batch, int32_t n_kv_heads, int32_t max_seq_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INTERATTN_AMD_H */

@@ -1,0 +1,124 @@
+// Shared device helpers for the gfx950 kernels: element codecs, DPP
+// cross-lane reductions inside 16-lane rows, and host-side error plumbing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <string>
+
+#include "../../include/interattn_amd.h"
+
+namespace ia {
+
+typedef uint32_t u32;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+// ------------------------------------------------------------------ element codecs
+
+__device__ __forceinline__ float bf16_lo(u32 w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(u32 w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ bf16x2_t as_bf16x2(u32 w) { return __builtin_bit_cast(bf16x2_t, w); }
+
+// Round-to-nearest-even float -> bf16 pair (lowers to v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
+  bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(u32, v);
+}
+
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float x) {
+  __bf16 h = (__bf16)x;
+  return __builtin_bit_cast(unsigned short, h);
+}
+
+// Four OCP e4m3fn codes in one word -> four floats (v_cvt_pk_f32_fp8).
+__device__ __forceinline__ void fp8x4_to_f32(u32 w, float* out) {
+  f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  out[0] = a[0];
+  out[1] = a[1];
+  out[2] = b[0];
+  out[3] = b[1];
+}
+
+// ------------------------------------------------------------------ DPP within 16-lane rows
+
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a row; every lane receives the total.  Partner sets
+// of mirror, half-mirror, xor2, xor1 are disjoint at each step.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<kDppRowMirror>(v);
+  v += dpp<kDppRowHalfMirror>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppXor1>(v);
+  return v;
+}
+
+template <int N, int CTRL>
+__device__ __forceinline__ void rs_step(float* v, bool sel) {
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const float lo = v[k], hi = v[k + N / 2];
+    const float keep = sel ? hi : lo;
+    const float send = sel ? lo : hi;
+    v[k] = keep + dpp<CTRL>(send);
+  }
+}
+
+// Reduce-scatter of NV per-lane partial sums over the 16 lanes of a row.
+// On return v[0 .. max(1, NV/16)) holds complete sums; with b = lane & 15 the
+// value index held in v[k] is
+//   NV=32: 2b + k,  NV=16: b,  NV=8: b >> 1,  NV=4: b >> 2.
+template <int NV>
+__device__ __forceinline__ void reduce_scatter16(float* v, int lane) {
+  static_assert(NV == 4 || NV == 8 || NV == 16 || NV == 32, "NV");
+  const int b = lane & 15;
+  rs_step<NV, kDppRowMirror>(v, b & 8);
+  rs_step<NV / 2, kDppRowHalfMirror>(v, b & 4);
+  if constexpr (NV >= 8) {
+    rs_step<NV / 4, kDppXor2>(v, b & 2);
+  } else {
+    v[0] += dpp<kDppXor2>(v[0]);
+  }
+  if constexpr (NV >= 16) {
+    rs_step<NV / 8, kDppXor1>(v, b & 1);
+  } else {
+    v[0] += dpp<kDppXor1>(v[0]);
+  }
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
+
+// Wave-level barrier for LDS traffic that stays inside one wavefront.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ------------------------------------------------------------------ host error plumbing
+
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace ia

@@ -1,0 +1,346 @@
+// Top-k block selection for gfx950: block scorer + per-(sequence, kv head)
+// radix select in one launch.
+//
+//   grid = (score chunks, Hkv, batch), 256 threads.  Each workgroup scores
+//   kChunk blocks of one (sequence, kv head): score_j = (mean_g q_g) . k_bar_j
+//   / sqrt(D), one k_bar row per 16 lanes (4 rows per wave-wide load), DPP
+//   row sums.  Scores go to global memory; the last workgroup of the (sequence,
+//   kv head) -- device-scope counter -- selects:
+//     * forced blocks: the first forced_first and last forced_last valid blocks;
+//     * the k_eff largest remaining scores by an MSB-first 8-bit radix select
+//       on order-preserving 32-bit keys (4 histogram passes in LDS), ties at
+//       the threshold taken in ascending block order;
+//     * an ordered compaction (wave ballots + LDS offsets) writes the chosen
+//       block ids in ascending order.
+//   The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
+//   with the mean key (k_bar) as the block representative.
+#include "ia_common.hpp"
+
+namespace ia {
+
+namespace {
+
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kChunk = 256;  // blocks scored per workgroup
+
+struct SelectParams {
+  const void* q;
+  int64_t q_batch_stride, q_row_stride;
+  const void* k_bar;
+  int64_t kb_batch_stride, kb_head_stride;
+  const int32_t* seq_lens;
+  int32_t block_size, nb_max, k, forced_first, forced_last, forced_in_k;
+  const int32_t* k_per_seq;  // optional [batch]
+  int32_t* idx;
+  int32_t k_cap;
+  int32_t* n_sel;
+  float* scores;  // [batch*Hkv, nb_max]
+  u32* counters;  // [batch*Hkv]
+  int32_t n_kv_heads;
+  float score_scale;  // 1 / (G * sqrt(D))
+};
+
+__device__ __forceinline__ u32 order_key(float s) {
+  const u32 u = __float_as_uint(s);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int D, int G, bool QF32, bool KBF16>
+__global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(SelectParams p) {
+  constexpr int DPL = D / 16;
+  __shared__ u32 hist[256];
+  __shared__ int sh_int[8];
+  __shared__ int wave_cnt[2][kSelWaves];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const int chunk = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int bh = b * p.n_kv_heads + h;
+
+  const int seq_len = max(p.seq_lens[b], 0);
+  const int nb = min((seq_len + p.block_size - 1) / p.block_size, p.nb_max);
+  const int n_chunks = max(1, (nb + kChunk - 1) / kChunk);
+  if (chunk >= n_chunks) return;
+
+  // ---- mean query of the group, this lane's dims
+  float qm[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) qm[e] = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      float v;
+      if constexpr (QF32) v = reinterpret_cast<const float*>(p.q)[row + e];
+      else v = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
+      qm[e] += v;
+    }
+  }
+
+  // ---- score this chunk: wave w handles rows j = chunk*kChunk + 4*(w + 4*step) + r
+  float* sc_row = p.scores + (int64_t)bh * p.nb_max;
+  const int j0 = chunk * kChunk;
+  const int j1 = min(nb, j0 + kChunk);
+  const char* kb = reinterpret_cast<const char*>(p.k_bar) +
+                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * (KBF16 ? 2 : 4);
+  for (int base = j0 + 4 * wave; base < j1; base += 4 * kSelWaves) {
+    const int j = base + r;
+    float a = 0.f;
+    if (j < j1) {
+      const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * (KBF16 ? 2 : 4);
+      if constexpr (KBF16) {
+        u32 w[DPL / 2];
+        if constexpr (DPL == 8) {
+          const uint4 v = *reinterpret_cast<const uint4*>(rowp);
+          w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(rowp);
+          w[0] = v.x; w[1] = v.y;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) {
+          a = fmaf(qm[2 * e], bf16_lo(w[e]), a);
+          a = fmaf(qm[2 * e + 1], bf16_hi(w[e]), a);
+        }
+      } else {
+        const float* fp = reinterpret_cast<const float*>(rowp);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], fp[e], a);
+      }
+    }
+    a = row16_sum(a);
+    if (c16 == 0 && j < j1) sc_row[j] = a * p.score_scale;
+  }
+  // blocks past this sequence's end read as -inf
+  if (chunk == n_chunks - 1) {
+    for (int j = nb + threadIdx.x; j < p.nb_max; j += kSelThreads) sc_row[j] = kNegInf;
+  }
+
+  // ---- last workgroup of (b, h) selects
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const u32 prev = atomicAdd(&p.counters[bh], 1u);
+    sh_int[0] = (prev == (u32)(n_chunks - 1));
+  }
+  __syncthreads();
+  if (!sh_int[0]) return;
+  __threadfence();
+
+  const int ff = min(max(p.forced_first, 0), nb);
+  const int fl_start = max(nb - max(p.forced_last, 0), 0);
+  auto is_forced = [&](int j) { return j < ff || j >= fl_start; };
+  const int n_forced = ff + (nb - max(fl_start, ff));  // |[0,ff) U [fl_start,nb)|
+  const int n_cand = nb - n_forced;
+  const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.k;
+  int k_eff = p.forced_in_k ? k_b - n_forced : k_b;
+  k_eff = max(k_eff, 0);
+  const int k_room = max(p.k_cap - n_forced, 0);
+  k_eff = min(k_eff, k_room);
+
+  u32 thr = 0u;       // threshold key; candidates with key > thr are taken
+  int take_ties = 0;  // number of candidates with key == thr taken (lowest indices first)
+  bool take_all = k_eff >= n_cand;
+  if (!take_all && k_eff > 0) {
+    u32 prefix = 0u, mask = 0u;
+    int remaining = k_eff;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[threadIdx.x] = 0u;
+      __syncthreads();
+      for (int j = threadIdx.x; j < nb; j += kSelThreads) {
+        if (is_forced(j)) continue;
+        const u32 key = order_key(sc_row[j]);
+        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // bins in descending order: lane l owns bins 255-4l .. 252-4l
+        u32 c[4];
+        u32 tot = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          c[t] = hist[255 - 4 * lane - t];
+          tot += c[t];
+        }
+        // inclusive scan over lanes (descending-bin order)
+        u32 inc = tot;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const u32 o = __shfl_up(inc, off, 64);
+          if (lane >= off) inc += o;
+        }
+        const u32 exc = inc - tot;
+        // the bin where the running count first reaches `remaining`
+        if (exc < (u32)remaining && inc >= (u32)remaining) {
+          u32 run = exc;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            if (run + c[t] >= (u32)remaining) {
+              sh_int[1] = 255 - 4 * lane - t;     // digit
+              sh_int[2] = remaining - (int)run;   // still needed inside this bin
+              break;
+            }
+            run += c[t];
+          }
+        }
+      }
+      __syncthreads();
+      const u32 digit = (u32)sh_int[1];
+      remaining = sh_int[2];
+      prefix |= digit << shift;
+      mask |= 255u << shift;
+      __syncthreads();
+    }
+    thr = prefix;
+    take_ties = remaining;
+  }
+
+  // ---- ordered compaction
+  int32_t* out_idx = p.idx + (int64_t)bh * p.k_cap;
+  int base_sel = 0, base_tie = 0;
+  for (int j0c = 0; j0c < nb; j0c += kSelThreads) {
+    const int j = j0c + threadIdx.x;
+    bool forced = false, above = false, tie = false;
+    if (j < nb) {
+      forced = is_forced(j);
+      if (!forced) {
+        if (take_all) {
+          above = true;
+        } else if (k_eff > 0) {
+          const u32 key = order_key(sc_row[j]);
+          above = key > thr;
+          tie = key == thr;
+        }
+      }
+    }
+    // tie rank in index order
+    const unsigned long long tb = __ballot(tie);
+    const int tie_rank_in_wave = __popcll(tb & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[1][wave] = __popcll(tb);
+    __syncthreads();
+    int tie_off = base_tie;
+    for (int w = 0; w < wave; ++w) tie_off += wave_cnt[1][w];
+    const bool take_tie = tie && (tie_off + tie_rank_in_wave < take_ties);
+    const bool sel = forced || above || take_tie;
+    const unsigned long long sb = __ballot(sel);
+    const int sel_rank = __popcll(sb & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[0][wave] = __popcll(sb);
+    __syncthreads();
+    int sel_off = base_sel;
+    for (int w = 0; w < wave; ++w) sel_off += wave_cnt[0][w];
+    if (sel && sel_off + sel_rank < p.k_cap) out_idx[sel_off + sel_rank] = j;
+    int tot_s = 0, tot_t = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+      tot_s += wave_cnt[0][w];
+      tot_t += wave_cnt[1][w];
+    }
+    base_sel += tot_s;
+    base_tie += tot_t;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    p.n_sel[bh] = min(base_sel, p.k_cap);
+    p.counters[bh] = 0u;
+  }
+}
+
+}  // namespace
+
+namespace {
+
+size_t select_ws_size(int batch, int hkv, int nb_max) {
+  const size_t bh = (size_t)batch * hkv;
+  return align_up(bh * 4, 256) + bh * (size_t)std::max(nb_max, 1) * 4;
+}
+
+template <int D, int G>
+int launch_select(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipStream_t st) {
+  if (qf32) {
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, true>), grid, dim3(kSelThreads), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, false>), grid, dim3(kSelThreads), 0, st, p);
+  } else {
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, true>), grid, dim3(kSelThreads), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, false>), grid, dim3(kSelThreads), 0, st, p);
+  }
+  return check_launch("select_topk");
+}
+
+}  // namespace
+}  // namespace ia
+
+extern "C" {
+
+size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t nb_max) {
+  return ia::select_ws_size(batch, n_kv_heads, nb_max);
+}
+
+int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
+                   int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens,
+                   int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq,
+                   int32_t forced_first, int32_t forced_last, int32_t forced_in_k, int32_t* idx, int32_t k_cap,
+                   int32_t* n_sel, float* scores, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace ia;
+  if (!shape) return fail(IA_ERR_INVALID, "shape is null");
+  if (shape->batch < 0 || shape->n_kv_heads <= 0 || shape->n_q_heads % shape->n_kv_heads != 0)
+    return fail(IA_ERR_INVALID, "n_q_heads must be a positive multiple of n_kv_heads");
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  if (D != 64 && D != 128) return fail(IA_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(IA_ERR_UNSUPPORTED, "GQA group size must be 1, 2, 4 or 8");
+  if (shape->q_dtype != IA_F32 && shape->q_dtype != IA_BF16) return fail(IA_ERR_INVALID, "q dtype");
+  if (k_bar_dtype != IA_F32 && k_bar_dtype != IA_BF16) return fail(IA_ERR_INVALID, "k_bar dtype must be IA_F32 or IA_BF16");
+  if (!q || !k_bar || !seq_lens || !idx || !n_sel) return fail(IA_ERR_INVALID, "null pointer argument");
+  if (block_size <= 0) return fail(IA_ERR_INVALID, "block_size must be positive");
+  if (nb_max < 0 || k < 0 || forced_first < 0 || forced_last < 0 || k_cap <= 0)
+    return fail(IA_ERR_INVALID, "nb_max, k, forced_* must be >= 0 and k_cap > 0");
+  const int eb = k_bar_dtype == IA_BF16 ? 2 : 4;
+  if ((kbar_batch_stride * eb) % 16 || (kbar_head_stride * eb) % 16 || reinterpret_cast<uintptr_t>(k_bar) % 16)
+    return fail(IA_ERR_INVALID, "k_bar rows must be 16-byte aligned");
+  const size_t need = select_ws_size(shape->batch, shape->n_kv_heads, nb_max);
+  if (!workspace || workspace_bytes < need)
+    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
+  if (shape->batch == 0) return IA_OK;
+  char* ws = reinterpret_cast<char*>(workspace);
+  const size_t bh = (size_t)shape->batch * shape->n_kv_heads;
+  SelectParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.k_bar = k_bar;
+  p.kb_batch_stride = kbar_batch_stride;
+  p.kb_head_stride = kbar_head_stride;
+  p.seq_lens = seq_lens;
+  p.block_size = block_size;
+  p.nb_max = nb_max;
+  p.k = k;
+  p.k_per_seq = k_per_seq;
+  p.forced_first = forced_first;
+  p.forced_last = forced_last;
+  p.forced_in_k = forced_in_k;
+  p.idx = idx;
+  p.k_cap = k_cap;
+  p.n_sel = n_sel;
+  p.counters = reinterpret_cast<u32*>(ws);
+  p.scores = scores ? scores : reinterpret_cast<float*>(ws + align_up(bh * 4, 256));
+  p.n_kv_heads = shape->n_kv_heads;
+  p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
+  const int n_chunks = std::max(1, (nb_max + kChunk - 1) / kChunk);
+  dim3 grid(n_chunks, shape->n_kv_heads, shape->batch);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const bool qf32 = shape->q_dtype == IA_F32;
+  const bool kbf16 = k_bar_dtype == IA_BF16;
+#define IA_SEL(DD, GG) \
+  if (D == DD && G == GG) return launch_select<DD, GG>(p, qf32, kbf16, grid, st);
+  IA_SEL(128, 4) IA_SEL(128, 8) IA_SEL(128, 2) IA_SEL(128, 1)
+  IA_SEL(64, 4) IA_SEL(64, 8) IA_SEL(64, 2) IA_SEL(64, 1)
+#undef IA_SEL
+  return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination");
+}
+
+}  // extern "C"

@@ -1,0 +1,323 @@
+"""Paged-pool entry points of the sparse decode-attention path (torch tensors in,
+HIP kernels underneath).
+
+Pool layout: ``pool_k, pool_v [n_pages, Hkv, page_size, D]`` (any page/head/token
+strides with contiguous rows), ``block_table [batch, max_pages] int32``,
+``seq_lens [batch] int32`` on the device.  Logical token ``t`` of sequence ``b`` is
+``pool[block_table[b, t // page_size], :, t % page_size]``.  fp8 pools are
+``torch.float8_e4m3fn`` with ``scales = (k_scale, v_scale)``, each ``[n_pages, Hkv]``
+float32.
+
+Every function launches on the current torch stream and never synchronises, except
+where a docstring says otherwise.  Scratch space lives in a caller-owned
+``workspace`` dict (the reference's ``_workspace_empty`` convention,
+CBT/core.py:558-570): tensors are created on first use (zero-filled), reused while
+the shapes match, and the kernels leave their counters zeroed for the next call.
+"""
+
+import math
+
+import torch
+
+from . import _native as N
+
+_DTYPE_CODE = {torch.float32: N.IA_F32, torch.bfloat16: N.IA_BF16}
+if hasattr(torch, "float8_e4m3fn"):
+    _DTYPE_CODE[torch.float8_e4m3fn] = N.IA_FP8_E4M3
+
+
+def _code(dtype, what):
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"{what}: unsupported dtype {dtype}") from None
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_cuda(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("interattn_amd kernels need device (cuda) tensors")
+
+
+def workspace_tensor(workspace, key, shape, *, device, dtype, zero=False):
+    """Reuse ``workspace[key]`` when shape/dtype/device match, else (re)create it.
+
+    Mirrors ``_workspace_empty`` (CBT/core.py:558-570); ``zero=True`` zero-fills a new
+    tensor (counters must start at zero; the kernels re-zero them after use)."""
+    shape = tuple(int(s) for s in shape)
+    make = torch.zeros if zero else torch.empty
+    if workspace is None:
+        return make(shape, device=device, dtype=dtype)
+    t = workspace.get(key)
+    if t is None or tuple(t.shape) != shape or t.device != device or t.dtype != dtype:
+        t = make(shape, device=device, dtype=dtype)
+        workspace[key] = t
+    return t
+
+
+def _scratch(workspace, key, nbytes, device):
+    t = workspace_tensor(workspace, key, (max(int(nbytes), 1),), device=device, dtype=torch.uint8, zero=True)
+    return t
+
+
+def _check_i32(t, name, shape=None):
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def paged_kv(pool_k, pool_v, block_table=None, scales=None):
+    """Describe a pool for the C ABI.  Returns ``(PagedKV, keepalive)``."""
+    _require_cuda(pool_k, pool_v, block_table)
+    if pool_k.dim() != 4 or pool_v.dim() != 4 or pool_k.shape != pool_v.shape:
+        raise ValueError("pool_k/pool_v must both be [n_pages, Hkv, page_size, D]")
+    if pool_k.dtype != pool_v.dtype:
+        raise ValueError("pool_k and pool_v must share a dtype")
+    if pool_k.stride(3) != 1 or pool_v.stride(3) != 1:
+        raise ValueError("pool rows (last dim) must be contiguous")
+    code = _code(pool_k.dtype, "pool")
+    n_pages, hkv, page, d = pool_k.shape
+    kv = N.PagedKV()
+    kv.k = pool_k.data_ptr()
+    kv.v = pool_v.data_ptr()
+    kv.dtype = code
+    kv.page_size = int(page)
+    kv.n_pages = int(n_pages)
+    kv.k_page_stride, kv.k_head_stride, kv.k_token_stride = (int(s) for s in pool_k.stride()[:3])
+    kv.v_page_stride, kv.v_head_stride, kv.v_token_stride = (int(s) for s in pool_v.stride()[:3])
+    keep = [pool_k, pool_v]
+    if block_table is not None:
+        _check_i32(block_table, "block_table")
+        if block_table.dim() != 2 or block_table.stride(1) != 1:
+            raise ValueError("block_table must be [batch, max_pages] with contiguous rows")
+        kv.block_table = block_table.data_ptr()
+        kv.bt_stride = int(block_table.stride(0)) if block_table.shape[0] > 1 else int(block_table.shape[1])
+        kv.bt_stride = max(kv.bt_stride, 1)
+        kv.bt_cols = int(block_table.shape[1])
+        keep.append(block_table)
+    if code == N.IA_FP8_E4M3:
+        if scales is None:
+            raise ValueError("fp8 pools need scales=(k_scale, v_scale), each [n_pages, Hkv] float32")
+        ks, vs = scales
+        for s_ in (ks, vs):
+            _require_cuda(s_)
+            if s_.dtype != torch.float32 or tuple(s_.shape) != (n_pages, hkv) or s_.stride(1) != 1:
+                raise ValueError("scales must be float32 [n_pages, Hkv] with contiguous rows")
+        if ks.stride(0) != vs.stride(0):
+            raise ValueError("k_scale and v_scale must share a layout")
+        kv.k_scale = ks.data_ptr()
+        kv.v_scale = vs.data_ptr()
+        kv.scale_page_stride = int(ks.stride(0))
+        keep += [ks, vs]
+    return kv, keep
+
+
+def _decode_shape(q, hkv):
+    if q.dim() != 3 or q.stride(2) != 1:
+        raise ValueError("q must be [batch, n_q_heads, D] with contiguous rows")
+    b, hq, d = q.shape
+    if hq % hkv != 0:
+        raise ValueError("n_q_heads must be a multiple of n_kv_heads (grouped query attention)")
+    sh = N.DecodeShape()
+    sh.batch = int(b)
+    sh.n_q_heads = int(hq)
+    sh.n_kv_heads = int(hkv)
+    sh.head_dim = int(d)
+    sh.q_batch_stride = int(q.stride(0))
+    sh.q_row_stride = int(q.stride(1))
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("q must be float32 or bfloat16")
+    sh.q_dtype = _code(q.dtype, "q")
+    return sh
+
+
+# --------------------------------------------------------------------------- summaries
+
+def build_block_summaries(pool_k, pool_v, block_table, seq_lens, block_size, *, nb_max, full=False,
+                          k_bar_dtype=torch.bfloat16, v_bar_dtype=torch.bfloat16, bounds_dtype=None,
+                          scales=None):
+    """Per-block summaries of the paged sequences (paged ``_build_prompt_blocks``,
+    CBT/core.py:449-500).  Returns a dict with ``k_bar [B, Hkv, nb_max, D]`` and
+    ``block_valid_counts [B, nb_max] int32``; with ``full=True`` also ``v_bar, k_max,
+    k_min`` (same shape), ``v_norm_max [B, Hkv, nb_max]`` and ``v_norm_all [B, Hkv]``."""
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    _require_cuda(seq_lens)
+    _check_i32(seq_lens, "seq_lens")
+    b = int(seq_lens.shape[0])
+    if block_table is not None and block_table.shape[0] != b:
+        raise ValueError("block_table rows must match seq_lens")
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    dev = pool_k.device
+    if bounds_dtype is None:
+        bounds_dtype = torch.float32 if pool_k.dtype == torch.float32 else torch.bfloat16
+    out = {
+        "k_bar": torch.empty((b, hkv, nb_max, d), device=dev, dtype=k_bar_dtype),
+        "block_valid_counts": torch.empty((b, nb_max), device=dev, dtype=torch.int32),
+    }
+    v_bar = k_max = k_min = vnm = vna = None
+    if full:
+        out["v_bar"] = v_bar = torch.empty((b, hkv, nb_max, d), device=dev, dtype=v_bar_dtype)
+        out["k_max"] = k_max = torch.empty((b, hkv, nb_max, d), device=dev, dtype=bounds_dtype)
+        out["k_min"] = k_min = torch.empty((b, hkv, nb_max, d), device=dev, dtype=bounds_dtype)
+        out["v_norm_max"] = vnm = torch.empty((b, hkv, nb_max), device=dev, dtype=torch.float32)
+        out["v_norm_all"] = vna = torch.empty((b, hkv), device=dev, dtype=torch.float32)
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = N.lib().ia_build_block_summaries(
+        kv, seq_lens.data_ptr(), b, hkv, d, int(block_size), int(nb_max),
+        p(out["k_bar"]), _code(k_bar_dtype, "k_bar"), p(v_bar), _code(v_bar_dtype, "v_bar"),
+        p(k_max), p(k_min), _code(bounds_dtype, "bounds"), p(vnm), p(vna),
+        out["block_valid_counts"].data_ptr(), _stream(pool_k))
+    N.check(rc)
+    del keep
+    return out
+
+
+# --------------------------------------------------------------------------- top-k selection
+
+def select_blocks_topk(q, k_bar, seq_lens, k, *, block_size, forced_first=0, forced_last=0,
+                       forced_in_k=False, k_cap=None, k_per_seq=None, return_scores=False, workspace=None):
+    """Top-k block selection per (sequence, kv head).
+
+    ``q [B, Hq, D]``, ``k_bar [B, Hkv, nb_max, D]`` (bf16/fp32 summaries).  Score =
+    group-mean ``q . k_bar / sqrt(D)`` (CBG/methods/quest.py:91-103).  Returns
+    ``(idx [B, Hkv, k_cap] int32, n_sel [B, Hkv] int32[, scores [B, Hkv, nb_max] f32])``;
+    ``idx[b, h, :n_sel[b, h]]`` are the chosen blocks in ascending order (forced first
+    ``forced_first`` / last ``forced_last`` blocks included; ``forced_in_k`` counts them
+    inside ``k``).  Ties at the k-th score go to the lower block index.  ``k_per_seq``
+    (int32 ``[B]`` on the device) overrides ``k`` per sequence; ``k_cap`` must then cover
+    its largest entry plus the forced blocks."""
+    _require_cuda(q, k_bar, seq_lens)
+    if k_bar.dim() != 4 or k_bar.stride(3) != 1 or k_bar.stride(2) != k_bar.shape[3]:
+        raise ValueError("k_bar must be [B, Hkv, nb_max, D] with contiguous blocks")
+    b, hkv, nb_max, d = (int(s) for s in k_bar.shape)
+    sh = _decode_shape(q, hkv)
+    if q.shape[0] != b or q.shape[2] != d:
+        raise ValueError("q and k_bar disagree on batch or head_dim")
+    _check_i32(seq_lens, "seq_lens", (b,))
+    if k < 0 or forced_first < 0 or forced_last < 0:
+        raise ValueError("k and forced block counts must be >= 0")
+    if k_per_seq is not None:
+        _require_cuda(k_per_seq)
+        _check_i32(k_per_seq, "k_per_seq", (b,))
+        if k_cap is None:
+            raise ValueError("k_per_seq needs an explicit k_cap")
+    if k_cap is None:
+        k_cap = max(int(k), forced_first + forced_last) if forced_in_k else int(k) + forced_first + forced_last
+    k_cap = max(int(k_cap), 1)
+    dev = q.device
+    idx = workspace_tensor(workspace, "topk_idx", (b, hkv, k_cap), device=dev, dtype=torch.int32)
+    n_sel = workspace_tensor(workspace, "topk_n_sel", (b, hkv), device=dev, dtype=torch.int32)
+    scores = None
+    if return_scores:
+        scores = workspace_tensor(workspace, "topk_scores", (b, hkv, nb_max), device=dev, dtype=torch.float32)
+    lib = N.lib()
+    ws_bytes = lib.ia_select_topk_workspace_size(b, hkv, nb_max)
+    ws = _scratch(workspace if workspace is not None else {}, "topk_scratch", ws_bytes, dev)
+    rc = lib.ia_select_topk(
+        sh, q.data_ptr(), k_bar.data_ptr(), _code(k_bar.dtype, "k_bar"), int(k_bar.stride(0)),
+        int(k_bar.stride(1)), seq_lens.data_ptr(), int(block_size), nb_max, int(k),
+        None if k_per_seq is None else k_per_seq.data_ptr(), int(forced_first),
+        int(forced_last), int(bool(forced_in_k)), idx.data_ptr(), k_cap, n_sel.data_ptr(),
+        None if scores is None else scores.data_ptr(), ws.data_ptr(), ws.numel(), _stream(q))
+    N.check(rc)
+    if return_scores:
+        return idx, n_sel, scores
+    return idx, n_sel
+
+
+# --------------------------------------------------------------------------- decode
+
+def _out_tensor(q, out, out_dtype, workspace):
+    dtype = q.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = workspace_tensor(workspace, "attention_output", tuple(q.shape), device=q.device, dtype=dtype)
+    if tuple(out.shape) != tuple(q.shape) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [batch, n_q_heads, D] tensor")
+    if out.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out must be float32 or bfloat16")
+    return out
+
+
+def sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, *, block_size, scale=None,
+                        scales=None, out=None, out_dtype=None, workspace=None):
+    """Attention over the selected blocks only: for each query row, softmax(q.K^T*scale)
+    over the valid tokens of blocks ``idx[b, h, :n_sel[b, h]]``, applied to V.  The
+    top-k form of the finalize stage (CBT/page_attention.py:206-255 + the split-K merge
+    of CBT/legacy.py:765-794).  Returns ``[B, Hq, D]`` (``out`` when given)."""
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    _require_cuda(q, seq_lens, idx, n_sel)
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    sh = _decode_shape(q, hkv)
+    b = int(q.shape[0])
+    if q.shape[2] != d:
+        raise ValueError("q head_dim does not match the pool")
+    _check_i32(seq_lens, "seq_lens", (b,))
+    _check_i32(n_sel, "n_sel", (b, hkv))
+    if idx.dim() != 3 or tuple(idx.shape[:2]) != (b, hkv) or not idx.is_contiguous():
+        raise ValueError("idx must be a contiguous [B, Hkv, k_cap] int32 tensor")
+    _check_i32(idx, "idx")
+    if block_table is not None and block_table.shape[0] != b:
+        raise ValueError("block_table rows must match the batch")
+    if not n_sel.is_contiguous():
+        raise ValueError("n_sel must be contiguous")
+    k_cap = int(idx.shape[2])
+    scale = d ** -0.5 if scale is None else float(scale)
+    out = _out_tensor(q, out, out_dtype, workspace)
+    lib = N.lib()
+    g = int(q.shape[1]) // hkv
+    items = lib.ia_sparse_max_items(b, hkv, k_cap)
+    ws_bytes = lib.ia_paged_decode_workspace_size(b, hkv, g, d, items)
+    ws = _scratch(workspace if workspace is not None else {}, "decode_scratch", ws_bytes, q.device)
+    rc = lib.ia_sparse_paged_decode(
+        sh, q.data_ptr(), kv, seq_lens.data_ptr(), int(block_size), idx.data_ptr(), k_cap, n_sel.data_ptr(),
+        scale, out.data_ptr(), _code(out.dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
+    N.check(rc)
+    del keep
+    return out
+
+
+def paged_decode(q, pool_k, pool_v, block_table, seq_lens, *, max_seq_len=None, scale=None, scales=None,
+                 out=None, out_dtype=None, workspace=None):
+    """Dense paged decode (the fallback path): softmax(q.K^T*scale).V over all
+    ``seq_lens[b]`` tokens.  ``max_seq_len`` must bound ``seq_lens``; when omitted it is
+    read back from the device (one host synchronisation)."""
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    _require_cuda(q, seq_lens)
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    sh = _decode_shape(q, hkv)
+    b = int(q.shape[0])
+    _check_i32(seq_lens, "seq_lens", (b,))
+    if block_table is not None and block_table.shape[0] != b:
+        raise ValueError("block_table rows must match the batch")
+    if max_seq_len is None:
+        max_seq_len = int(seq_lens.max().item()) if b else 0
+    scale = d ** -0.5 if scale is None else float(scale)
+    out = _out_tensor(q, out, out_dtype, workspace)
+    lib = N.lib()
+    g = int(q.shape[1]) // hkv
+    items = lib.ia_dense_max_items(b, hkv, int(max_seq_len))
+    ws_bytes = lib.ia_paged_decode_workspace_size(b, hkv, g, d, items)
+    ws = _scratch(workspace if workspace is not None else {}, "dense_scratch", ws_bytes, q.device)
+    rc = lib.ia_paged_decode(sh, q.data_ptr(), kv, seq_lens.data_ptr(), int(max_seq_len), scale,
+                             out.data_ptr(), _code(out.dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
+    N.check(rc)
+    del keep
+    return out
+
+
+def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, block_size, forced_first=0,
+                       forced_last=0, forced_in_k=False, scale=None, scales=None, out=None, workspace=None):
+    """One decode-attention layer call of the top-k path: select, then finalize."""
+    idx, n_sel = select_blocks_topk(q, k_bar, seq_lens, k, block_size=block_size, forced_first=forced_first,
+                                    forced_last=forced_last, forced_in_k=forced_in_k, workspace=workspace)
+    return sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, block_size=block_size,
+                               scale=scale, scales=scales, out=out, workspace=workspace)
+
+
+def nb_for(seq_len, block_size):
+    return int(math.ceil(int(seq_len) / int(block_size)))

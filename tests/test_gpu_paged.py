@@ -1,0 +1,283 @@
+"""GPU parity of the paged top-k path against the CPU oracle at oracle-sized shapes.
+
+Bars: selected block indices equal except near-ties (scores
+within 1e-3 relative of the k-th admitted score); outputs within 2e-2 abs for bf16
+and 1e-4 abs for fp32.  fp8 K/V: within 2e-3 abs of the oracle run on the
+dequantised values (the kernel's products are exact; only accumulation order and
+the bf16 output rounding differ) and within 6e-2 abs of the bf16 result.
+"""
+
+import math
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import interattn_amd as ia
+from oracle import attention as A
+from oracle import select as S
+from oracle import summaries as Su
+from oracle.cases import make_case
+from oracle.paged import paged_gather
+from tests._util import announce, check_indices, oracle_summaries, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": 2e-2, "f32": 1e-4}
+
+# name, batch, hq, hkv, d, seq_lens, page, block, dtype, (k, forced_first, forced_last, in_k), outlier
+CASES = [
+    ("c1_f32", 1, 8, 2, 64, [2048], 64, 64, "f32", (8, 0, 1, True), False),
+    ("c2_small", 1, 32, 8, 128, [4133], 16, 64, "bf16", (16, 1, 2, False), True),
+    ("ragged_b3", 3, 32, 8, 128, [1000, 64, 3333], 16, 64, "bf16", (8, 0, 0, False), False),
+    ("g8_d64", 2, 16, 2, 64, [500, 777], 32, 32, "bf16", (5, 1, 1, False), False),
+    ("g2_b16", 2, 4, 2, 128, [300, 129], 16, 16, "bf16", (6, 0, 2, True), False),
+    ("g1_b128", 1, 2, 2, 128, [1257], 64, 128, "bf16", (3, 1, 0, False), False),
+    ("block256", 1, 8, 2, 128, [2000], 16, 256, "bf16", (2, 0, 1, False), False),
+    ("c4_small", 2, 32, 8, 128, [8192, 6000], 16, 128, "bf16", (16, 0, 0, False), False),
+    ("f32_d128", 2, 8, 2, 128, [700, 333], 32, 32, "f32", (4, 1, 1, False), False),
+]
+IDS = [c[0] for c in CASES]
+
+
+def _build(c, fp8=False):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, outlier = c
+    case = make_case(seed=zlib.crc32(name.encode()) % 10000, batch=b, hq=hq, hkv=hkv, d=d, seq_lens=lens, page_size=page,
+                     dtype=dt, k_outlier=outlier, fp8=fp8)
+    return case
+
+
+def _k_cap(sel):
+    k, ff, fl, in_k = sel
+    return max(k, ff + fl) if in_k else k + ff + fl
+
+
+def _torch_dtype(dt):
+    return torch.float32 if dt == "f32" else torch.bfloat16
+
+
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_summaries_match_oracle(c, device):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    announce(f"summaries {name}")
+    case = _build(c)
+    dev = to_dev(case, device, _torch_dtype(dt))
+    nb_max = max(math.ceil(L / block) for L in lens)
+    kb_dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    got = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                   nb_max=nb_max, full=True, k_bar_dtype=kb_dtype, v_bar_dtype=kb_dtype)
+    torch.cuda.synchronize()
+    for i, L in enumerate(lens):
+        ref = Su.build_block_summaries(case["k"][i], case["v"][i], block)
+        n = ref["block_valid_counts"].shape[0]
+        assert np.array_equal(got["block_valid_counts"][i, :n].cpu().numpy(), ref["block_valid_counts"])
+        assert np.all(got["block_valid_counts"][i, n:].cpu().numpy() == 0)
+        tol = 1e-5 if dt == "f32" else 2 ** -7
+        for key in ("k_bar", "v_bar"):
+            g = got[key][i, :, :n].float().cpu().numpy()
+            np.testing.assert_allclose(g, ref[key], rtol=tol, atol=1e-5, err_msg=key)
+        for key in ("k_max", "k_min"):
+            assert np.array_equal(got[key][i, :, :n].float().cpu().numpy(), ref[key]), key
+        np.testing.assert_allclose(got["v_norm_max"][i, :, :n].cpu().numpy(), ref["v_norm_max"], rtol=1e-5)
+        np.testing.assert_allclose(got["v_norm_all"][i].cpu().numpy(), ref["v_norm_all"], rtol=1e-5)
+        if n < nb_max:
+            assert torch.isneginf(got["v_norm_max"][i, :, n:]).all()
+
+
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_select_topk_matches_oracle(c, device):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    k, ff, fl, in_k = sel
+    announce(f"select_topk {name}")
+    case = _build(c)
+    kb, counts, _ = oracle_summaries(case, block, k_bar_dtype="f32" if dt == "f32" else "bf16")
+    q = torch.from_numpy(case["q"]).to(device=device, dtype=_torch_dtype(dt))
+    kb_t = torch.from_numpy(kb).to(device=device, dtype=_torch_dtype(dt))
+    seq_lens = torch.from_numpy(case["seq_lens"]).to(device)
+    idx, n_sel, scores = ia.select_blocks_topk(q, kb_t, seq_lens, k, block_size=block, forced_first=ff,
+                                               forced_last=fl, forced_in_k=in_k, return_scores=True)
+    torch.cuda.synchronize()
+    idx, n_sel, scores = idx.cpu().numpy(), n_sel.cpu().numpy(), scores.cpu().numpy()
+    qf = case["q"].astype(np.float64)
+    for i, L in enumerate(lens):
+        nb = math.ceil(L / block)
+        ref_sc = S.topk_block_scores(qf[i], kb[i], counts[i], hq // hkv)
+        np.testing.assert_allclose(scores[i, :, :nb], ref_sc[:, :nb], rtol=1e-5, atol=1e-5)
+        assert np.all(np.isneginf(scores[i, :, nb:]))
+        for h in range(hkv):
+            check_indices(idx[i, h], n_sel[i, h], ref_sc[h, :nb], nb, k, ff, fl, in_k)
+
+
+def _oracle_idx(case, block, sel, hkv, group, kb_dtype):
+    k, ff, fl, in_k = sel
+    kb, counts, _ = oracle_summaries(case, block, k_bar_dtype=kb_dtype)
+    out = []
+    for i, L in enumerate(case["seq_lens"]):
+        nb = math.ceil(int(L) / block)
+        sc = S.topk_block_scores(case["q"][i].astype(np.float64), kb[i], counts[i], group)
+        out.append([S.select_topk(sc[h, :nb], nb, k, ff, fl, in_k) for h in range(hkv)])
+    return out
+
+
+def _pack_idx(per_seq, k_cap, device):
+    b, hkv = len(per_seq), len(per_seq[0])
+    idx = np.full((b, hkv, k_cap), -1, np.int32)
+    n = np.zeros((b, hkv), np.int32)
+    for i in range(b):
+        for h in range(hkv):
+            s = per_seq[i][h]
+            idx[i, h, :len(s)] = s
+            n[i, h] = len(s)
+    return torch.from_numpy(idx).to(device), torch.from_numpy(n).to(device)
+
+
+@pytest.mark.parametrize("out_f32", [False, True])
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_sparse_decode_matches_oracle(c, out_f32, device):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    announce(f"sparse_decode {name} out_f32={out_f32}")
+    case = _build(c)
+    dev = to_dev(case, device, _torch_dtype(dt))
+    per_seq = _oracle_idx(case, block, sel, hkv, hq // hkv, "f32" if dt == "f32" else "bf16")
+    idx, n_sel = _pack_idx(per_seq, _k_cap(sel), device)
+    out = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                 idx, n_sel, block_size=block, out_dtype=torch.float32 if out_f32 else None)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    tol = TOL[dt]
+    for i, L in enumerate(lens):
+        ref = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], per_seq[i], block, p_bf16=(dt == "bf16"))
+        err = np.abs(got[i] - ref).max()
+        assert err <= tol, f"seq {i}: max abs err {err}"
+
+
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_dense_decode_matches_oracle(c, device):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    announce(f"dense_decode {name}")
+    case = _build(c)
+    dev = to_dev(case, device, _torch_dtype(dt))
+    out = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                          max_seq_len=max(lens))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    for i, L in enumerate(lens):
+        ref = A.dense_decode(case["q"][i], case["k"][i], case["v"][i])
+        err = np.abs(got[i] - ref).max()
+        assert err <= TOL[dt], f"seq {i}: max abs err {err}"
+
+
+FP8_CASES = [
+    ("c5_small", 2, 32, 8, 128, [4096, 3000], 16, 128, "bf16", (8, 0, 0, False), False),
+    ("fp8_d64_g8", 2, 16, 2, 64, [777, 64], 32, 32, "bf16", (4, 1, 1, False), False),
+]
+
+
+@pytest.mark.skipif(not hasattr(torch, "float8_e4m3fn"), reason="torch without float8")
+@pytest.mark.parametrize("c", FP8_CASES, ids=[c[0] for c in FP8_CASES])
+def test_fp8_paths_match_oracle(c, device):
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    announce(f"fp8 {name}")
+    case = _build(c, fp8=True)
+    dev = to_dev(case, device, fp8=True)
+    per_seq = _oracle_idx(case, block, sel, hkv, hq // hkv, "bf16")
+    idx, n_sel = _pack_idx(per_seq, _k_cap(sel), device)
+    out = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                 idx, n_sel, block_size=block, scales=dev["scales"])
+    dense = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                            max_seq_len=max(lens), scales=dev["scales"])
+    # the bf16 reference: same inputs before quantisation
+    case_bf = _build(c)
+    dev_bf = to_dev(case_bf, device, torch.bfloat16)
+    out_bf = ia.sparse_paged_decode(dev_bf["q"], dev_bf["pool_k"], dev_bf["pool_v"], dev_bf["block_table"],
+                                    dev_bf["seq_lens"], idx, n_sel, block_size=block)
+    torch.cuda.synchronize()
+    got, gd, gbf = out.float().cpu().numpy(), dense.float().cpu().numpy(), out_bf.float().cpu().numpy()
+    for i, L in enumerate(lens):
+        ref = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], per_seq[i], block)
+        assert np.abs(got[i] - ref).max() <= 2e-3 + 2 ** -8 * np.abs(ref).max()
+        refd = A.dense_decode(case["q"][i], case["k"][i], case["v"][i])
+        assert np.abs(gd[i] - refd).max() <= 2e-3 + 2 ** -8 * np.abs(refd).max()
+        assert np.abs(got[i] - gbf[i]).max() <= 6e-2
+
+
+def test_fp8_codec_on_device(device):
+    """v_cvt_pk_f32_fp8 decodes OCP e4m3fn: a kernel that sees every code once."""
+    if not hasattr(torch, "float8_e4m3fn"):
+        pytest.skip("torch without float8")
+    announce("fp8 codec")
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes = codes[(codes & 0x7F) != 0x7F]          # drop NaN codes
+    n = codes.numel()                               # 254 codes
+    page, d = 16, 128
+    pool = torch.zeros((1, 1, page, d), dtype=torch.uint8)
+    flat = pool.view(-1)
+    flat[:n] = codes
+    pool_k = pool.to(device).view(torch.float8_e4m3fn)
+    pool_v = torch.zeros_like(pool_k)
+    one = torch.ones((1, 1), device=device, dtype=torch.float32)
+    seq = torch.tensor([page], device=device, dtype=torch.int32)
+    s = ia.build_block_summaries(pool_k, pool_v, None, seq, 16, nb_max=1, full=True,
+                                 k_bar_dtype=torch.float32, bounds_dtype=torch.float32, scales=(one, one))
+    torch.cuda.synchronize()
+    vals = torch.from_numpy(pool.numpy()).view(torch.float8_e4m3fn).float().view(page, d)
+    assert torch.equal(s["k_max"][0, 0, 0].cpu(), vals.max(0).values)
+    assert torch.equal(s["k_min"][0, 0, 0].cpu(), vals.min(0).values)
+    # with max, min and the (exact) mean of the two non-zero codes per dim, every code is pinned
+    assert torch.equal(s["k_bar"][0, 0, 0].cpu(), vals.sum(0) / page)
+
+
+def test_edge_cases(device):
+    announce("edge cases")
+    hq, hkv, d, page, block = 8, 2, 128, 16, 32
+    case = make_case(seed=99, batch=4, hq=hq, hkv=hkv, d=d, seq_lens=[0, 1, 40, 96], page_size=page)
+    dev = to_dev(case, device)
+    # sequence 3: poison its last page id (out of range) -> that page is skipped
+    bt = dev["block_table"].clone()
+    bt[3, 5] = 10 ** 6
+    kb, counts, _ = oracle_summaries(case, block)
+    kb_t = torch.from_numpy(kb).to(device=device, dtype=torch.bfloat16)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], kb_t, dev["seq_lens"], 2, block_size=block, forced_last=1)
+    out = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], bt, dev["seq_lens"], idx, n_sel,
+                                 block_size=block)
+    zero_k = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], bt, dev["seq_lens"], idx,
+                                    torch.zeros_like(n_sel), block_size=block)
+    dense = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], bt, dev["seq_lens"], max_seq_len=96)
+    torch.cuda.synchronize()
+    n_sel = n_sel.cpu().numpy()
+    assert n_sel[0].tolist() == [0, 0]                      # empty sequence selects nothing
+    assert n_sel[1].tolist() == [1, 1]
+    assert torch.all(out[0] == 0) and torch.all(zero_k == 0) and torch.all(dense[0] == 0)
+    got = out.float().cpu().numpy()
+    idx = idx.cpu().numpy()
+    for i in (1, 2):
+        sel = [idx[i, h, :n_sel[i, h]] for h in range(hkv)]
+        ref = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], sel, block, p_bf16=True)
+        assert np.abs(got[i] - ref).max() <= 2e-2
+    # seq 3 without its 6th page (tokens 80..95)
+    k3, v3 = case["k"][3][:, :80], case["v"][3][:, :80]
+    ref = A.dense_decode(case["q"][3], k3, v3)
+    assert np.abs(dense[3].float().cpu().numpy() - ref).max() <= 2e-2
+
+
+def test_workspace_reuse_and_counters_rearm(device):
+    """Repeated calls on one workspace give identical results (counters re-armed)."""
+    announce("workspace reuse")
+    c = CASES[7]
+    case = _build(c)
+    dev = to_dev(case, device)
+    block = c[7]
+    kb, counts, _ = oracle_summaries(case, block)
+    kb_t = torch.from_numpy(kb).to(device=device, dtype=torch.bfloat16)
+    ws = {}
+    outs = []
+    for _ in range(3):
+        o = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                  kb_t, 16, block_size=block, workspace=ws)
+        outs.append(o.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    for key in ("topk_scratch", "decode_scratch"):
+        cnt = ws[key][:64].view(torch.int32)
+        assert torch.all(cnt == 0), key

@@ -1,0 +1,68 @@
+"""The C ABI library loads and exports every symbol ``include/interattn_amd.h`` declares,
+and rejects bad arguments before touching the GPU (CPU only: no compute calls)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from interattn_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "interattn_amd.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"IA_API\s+[\w\s\*]*?\b(ia_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_symbols():
+    syms = header_symbols()
+    assert syms, "no IA_API declarations found"
+    assert set(syms) == set(N.SIGNATURES), "ctypes signatures and header declarations differ"
+
+
+def test_library_exports_every_header_symbol():
+    lib = N.lib()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    assert lib.ia_version() >= 1
+
+
+def test_struct_layouts_match_the_header():
+    # ia_paged_kv: 2 pointers, 2 int32, 7 int64, pointer, 2 int64, 2 pointers, int64
+    assert ctypes.sizeof(N.PagedKV) == 8 * 2 + 4 * 2 + 8 * 7 + 8 + 8 * 2 + 8 * 2 + 8
+    assert ctypes.sizeof(N.DecodeShape) == 4 * 4 + 8 * 2 + 8
+
+
+def test_workspace_sizes_are_consistent():
+    lib = N.lib()
+    assert lib.ia_select_topk_workspace_size(16, 8, 1024) >= 16 * 8 * 1024 * 4
+    items = lib.ia_sparse_max_items(16, 8, 64)
+    assert 1 <= items <= 64
+    need = lib.ia_paged_decode_workspace_size(16, 8, 4, 128, items)
+    assert need >= 16 * 8 * items * 4 * 128 * 4
+    assert lib.ia_dense_max_items(1, 8, 0) == 1
+
+
+def test_invalid_arguments_are_rejected_without_launching():
+    lib = N.lib()
+    sh = N.DecodeShape(batch=1, n_q_heads=6, n_kv_heads=4, head_dim=128, q_batch_stride=0, q_row_stride=128,
+                       q_dtype=N.IA_BF16)
+    kv = N.PagedKV()
+    rc = lib.ia_sparse_paged_decode(sh, None, kv, None, 64, None, 8, None, 1.0, None, N.IA_BF16, None, 0, None)
+    assert rc != 0
+    assert lib.ia_last_error()
+    sh.n_q_heads = 32
+    sh.n_kv_heads = 8
+    sh.head_dim = 96
+    rc = lib.ia_select_topk(sh, None, None, N.IA_BF16, 0, 0, None, 64, 8, 4, None, 0, 0, 0, None, 4, None, None,
+                            None, 0, None)
+    assert rc != 0
+    with pytest.raises(ValueError):
+        N.check(rc)
+    rc = lib.ia_build_block_summaries(kv, None, 1, 8, 128, 64, 4, None, 1, None, 1, None, None, 1, None, None, None,
+                                      None)
+    assert rc == N.IA_ERR_INVALID

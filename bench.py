@@ -107,11 +107,30 @@ def algorithmic_bytes(w, lens, n_sel_list):
     for b, L in enumerate(lens):
         for h in range(hkv):
             for j in n_sel_list[b][h]:
-                toks = min(block, L - j * block)
+                toks = min(block, L - int(j) * block)
                 kv += toks * d * 2 * s_kv
                 if w["kv"] == "fp8":
                     scales += math.ceil(toks / page) * 2 * 4
-    return qo, summ, kv + scales
+    return int(qo), int(summ), int(kv + scales)
+
+
+def copy_ceiling_gbps(dev, nbytes=4 << 30, reps=10):
+    """Measured device copy bandwidth (read + write bytes / time) of a plain
+    ``copy_`` over ``nbytes``: the practical HBM ceiling beside the 8 TB/s peak."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    sec = start.elapsed_time(end) / 1e3 / reps
+    del src, dst
+    return 2 * nbytes / sec / 1e9
 
 
 def time_events(fn, n, stream):
@@ -302,6 +321,7 @@ def main():
 
         dense_us = time_events(run_dense, 3, stream) * 1e3 / nl
 
+    copy_gbps = copy_ceiling_gbps(dev)
     s_kv = 1 if w["kv"] == "fp8" else 2
     dense_bytes = qo_b + sum(w["hkv"] * L * w["d"] * 2 * s_kv for L in lens)
 
@@ -342,6 +362,8 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "ia_condition_block_paged_finalize", "achieved": round(fin_gbps, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(fin_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": None},
+        "copy_ceiling_GBps": round(copy_gbps, 1),
+        "finalize_frac_of_copy": round(fin_gbps / copy_gbps, 4),
         "dense_us": None if dense_us is None else round(dense_us, 2),
         "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
         "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us_per_layer, 2),

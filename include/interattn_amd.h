@@ -8,9 +8,10 @@
  * non-zero IA_ERR_* code.  ia_last_error() returns the message of the last
  * failure on the calling thread.  Scratch memory comes from a caller-owned
  * workspace whose size is given by the matching *_workspace_size() function;
- * the workspace must be zero-filled once before its first use, and every entry
- * point leaves its counters zeroed again for the next call.  Calls that share
- * one workspace must not overlap.
+ * its contents need no initialisation.  Calls that share one workspace must not
+ * overlap.  No kernel synchronises across workgroups inside a launch: multi-step
+ * work (score -> select, split-K partials -> merge) is ordered by kernel
+ * boundaries on the caller's stream.
  *
  * Reference paths below are relative to the reference repository root;
  * CBT = llama/script/analysis/condition_block_gen/methods/condition_block_triton_impl,

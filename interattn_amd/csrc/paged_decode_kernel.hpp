@@ -1,0 +1,645 @@
+// Paged decode attention for gfx950: the selected-block finalize (sparse) and
+// the dense fallback share one kernel template.
+//
+// Work decomposition
+//   grid = (items, Hkv, batch); one 256-thread workgroup (4 waves) per split-K
+//   item of one (sequence, kv head).  An item is a run of "units": selected
+//   blocks (sparse) or 128-token tiles (dense).  A prologue stages the item's
+//   unit token ranges and one page id per 16-token subtile in LDS (so the
+//   streaming loop never waits on a dependent scalar load).  Waves take units
+//   round-robin and stream them one page-resident subtile at a time, keeping
+//   their own online-softmax state; the workgroup folds its four waves in LDS
+//   and writes one (m, l, acc) partial (an empty partial when the (sequence,
+//   kv head) needs fewer items than the grid row), or the output rows directly
+//   when the grid has a single item per row.  A second small kernel merges the
+//   partials.
+//   There is no cross-workgroup synchronisation inside a launch.
+//
+// Lane layout (head_dim D, DPL = D/16 dims per lane)
+//   lane = 16*r + c.  A subtile is read as four steps i = 0..3; in step i, row
+//   r holds token 4i + r and lane c holds dims [c*DPL, (c+1)*DPL): one
+//   contiguous 4-token load per wave per step (1 KiB for bf16 D=128).  K and V
+//   of the next subtiles are in flight in a ring of register buffers while the
+//   current one is consumed (two subtiles, 16 KiB per wave, for bf16).  Q.K
+//   partial sums for the 4 steps x G query rows are
+//   reduce-scattered over the 16-lane row with DPP, leaving each lane the
+//   complete score of one (token, query row) pair; the softmax weights reach
+//   the V lanes of the same row through DPP row broadcasts (row_newbcast).
+//
+// Numerics follow the reference's fused kernel (CBT/page_attention.py):
+//   bf16 K/V: scores = bf16(q) . K in fp32 (v_dot2_f32_bf16), fp32 online
+//   softmax, weights rounded to bf16 for the P.V product (:248-252), fp32
+//   normaliser (:253).  fp32 K/V: everything in fp32.  fp8 K/V: codes are
+//   widened to fp32, the per-(page, head) scale multiplies the score and the
+//   weight.
+#pragma once
+
+#include "ia_common.hpp"
+
+namespace ia {
+
+// kRing: register buffers in the load pipeline (subtiles in flight = kRing - 1),
+// sized so a wave stays within 256 registers (two waves per SIMD).
+struct KvBf16 {
+  static constexpr int kBytes = 2;
+  static constexpr int kRing = 3;
+};
+struct KvF32 {
+  static constexpr int kBytes = 4;
+  static constexpr int kRing = 2;
+};
+struct KvFp8 {
+  static constexpr int kBytes = 1;
+  static constexpr int kRing = 4;
+};
+
+template <int NWD>
+__device__ __forceinline__ void load_words(const char* p, u32* w) {
+  if constexpr (NWD == 8) {
+    const uint4 a = reinterpret_cast<const uint4*>(p)[0];
+    const uint4 b = reinterpret_cast<const uint4*>(p)[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else if constexpr (NWD == 4) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (NWD == 2) {
+    const uint2 a = *reinterpret_cast<const uint2*>(p);
+    w[0] = a.x; w[1] = a.y;
+  } else {
+    w[0] = *reinterpret_cast<const u32*>(p);
+  }
+}
+
+struct DecodeParams {
+  const void* q;
+  int64_t q_batch_stride, q_row_stride;
+  ia_paged_kv kv;
+  const int32_t* seq_lens;
+  const int32_t* idx;  // sparse only
+  const int32_t* n_sel;
+  int32_t k_cap;
+  int32_t unit_tokens;  // tokens per unit: block_size (sparse) or the dense tile
+  int32_t upi;          // units per item
+  int32_t max_items;
+  int32_t n_kv_heads;
+  float scale_log2;  // softmax scale * log2(e)
+  int32_t q_f32;     // q is fp32 (else bf16)
+  int32_t out_f32;   // out is fp32 (else bf16)
+  void* out;
+  float* part_ml;  // [batch*Hkv, max_items, G, 2]
+  float* part_acc; // [batch*Hkv, max_items, G, D]
+};
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kDenseTile = 128;
+constexpr int kMaxUnitsPerItem = 512;  // LDS unit ranges per item
+constexpr int kMaxSubsPerItem = 2048;  // LDS page ids per item (16 tokens each)
+
+// Lane (within the 16-lane row) and slot holding the reduce-scattered value of
+// index x = i*G + g (see reduce_scatter16).
+template <int G>
+struct ScoreMap {
+  static constexpr int NV = 4 * G;
+  static constexpr int KG = NV >= 16 ? NV / 16 : 1;
+  static constexpr int lane_of(int x) { return NV >= 16 ? x / (NV / 16) : x * (16 / NV); }
+  static constexpr int slot_of(int x) { return NV >= 16 ? x % (NV / 16) : 0; }
+};
+
+template <int CTRL>
+__device__ __forceinline__ float bcast_row(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// max / sum over the lanes that hold the same query row g
+template <int G, bool MAX>
+__device__ __forceinline__ float fold_g(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  v = op(v, dpp<kDppRowRor4>(v));
+  v = op(v, dpp<kDppRowRor8>(v));
+  if constexpr (G <= 2) v = op(v, dpp<kDppXor1>(v));
+  if constexpr (G == 1) v = op(v, dpp<kDppXor2>(v));
+  v = op(v, shfl_xor_f(v, 16));
+  v = op(v, shfl_xor_f(v, 32));
+  return v;
+}
+
+template <int G, int D>
+__device__ __forceinline__ void store_decode_out(const DecodeParams& p, int b, int h, int o, float v) {
+  const int g = o / D, d = o % D;
+  const int64_t off = ((int64_t)b * (p.n_kv_heads * G) + h * G + g) * D + d;
+  if (p.out_f32) {
+    reinterpret_cast<float*>(p.out)[off] = v;
+  } else {
+    reinterpret_cast<unsigned short*>(p.out)[off] = f32_to_bf16_bits(v);
+  }
+}
+
+// Softmax-weight rescale factor of query row g, taken from the lane of the
+// same quad that owns g (quad_perm broadcast [q,q,q,q] = q * 0x55).
+template <int G>
+__device__ __forceinline__ float alpha_of_row(const float* alpha, int g) {
+  if constexpr (G == 4) {
+    switch (g) {
+      case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0x00, 0xf, 0xf, false));
+      case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0x55, 0xf, 0xf, false));
+      case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0xAA, 0xf, 0xf, false));
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0xFF, 0xf, 0xf, false));
+    }
+  } else if constexpr (G == 8) {  // g = 2*(c16 & 3) + k
+    const float v = (g & 1) ? alpha[1] : alpha[0];
+    switch (g >> 1) {
+      case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x00, 0xf, 0xf, false));
+      case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x55, 0xf, 0xf, false));
+      case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xAA, 0xf, 0xf, false));
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xFF, 0xf, 0xf, false));
+    }
+  } else if constexpr (G == 2) {  // g = (c16 >> 1) & 1: quad lanes 2g, 2g+1
+    return g ? __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0xAA, 0xf, 0xf, false))
+             : __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(alpha[0]), 0x00, 0xf, 0xf, false));
+  } else {
+    return alpha[0];
+  }
+}
+
+// pb[i][g] = weight of (token 4i + r, row g), read from the row lane that owns
+// index x = i*G + g after the reduce-scatter (compile-time lane and slot).
+template <int G, int X>
+struct WeightBcast {
+  __device__ __forceinline__ static void run(const float* pw, float (*pb)[G]) {
+    WeightBcast<G, X - 1>::run(pw, pb);
+    constexpr int x = X - 1;
+    constexpr int L = ScoreMap<G>::lane_of(x);
+    constexpr int S = ScoreMap<G>::slot_of(x);
+    pb[x / G][x % G] = bcast_row<0x150 + L>(pw[S]);
+  }
+};
+template <int G>
+struct WeightBcast<G, 0> {
+  __device__ __forceinline__ static void run(const float*, float (*)[G]) {}
+};
+
+template <int D, int G, typename KV, bool SPARSE>
+__global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(DecodeParams p) {
+  constexpr int DPL = D / 16;
+  constexpr int NWD = DPL * KV::kBytes / 4;
+  using SM = ScoreMap<G>;
+  constexpr int NV = SM::NV;
+  constexpr int KG = SM::KG;
+  constexpr bool kBf16 = KV::kBytes == 2;
+  constexpr bool kFp8 = KV::kBytes == 1;
+
+  __shared__ int unit_lo[kMaxUnitsPerItem];
+  __shared__ int unit_hi[kMaxUnitsPerItem];
+  __shared__ int sub_page[kMaxSubsPerItem];
+  __shared__ float wacc_lds[kWaves][G * D];
+  __shared__ float wm_lds[kWaves][G];
+  __shared__ float wl_lds[kWaves][G];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const int item = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int bh = b * p.n_kv_heads + h;
+
+  const int seq_len = max(p.seq_lens[b], 0);
+  int n_units;
+  if constexpr (SPARSE) {
+    n_units = min(max(p.n_sel[bh], 0), p.k_cap);
+  } else {
+    n_units = (seq_len + p.unit_tokens - 1) / p.unit_tokens;
+  }
+  const int n_items = max(1, min(p.max_items, (n_units + p.upi - 1) / p.upi));
+  const bool split = gridDim.x > 1;  // partials + merge kernel, else direct output
+  if (item >= n_items) {
+    // an empty slot: the merge reads every slot of the grid row
+    if (threadIdx.x < G) {
+      const int64_t slot = (int64_t)bh * p.max_items + item;
+      p.part_ml[(slot * G + threadIdx.x) * 2 + 0] = kNegInf;
+      p.part_ml[(slot * G + threadIdx.x) * 2 + 1] = 0.f;
+    }
+    return;
+  }
+
+  const ia_paged_kv& kv = p.kv;
+  const int page_size = kv.page_size;
+  const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
+  const int u_begin = item * p.upi;
+  const int nu = max(0, min(n_units, u_begin + p.upi) - u_begin);
+  const int nsub_u = (p.unit_tokens + 15) / 16;
+
+  // ---- prologue: token ranges of this item's units, then one page id per subtile
+  for (int t = threadIdx.x; t < nu; t += kThreads) {
+    int lo = 0, hi = 0;
+    if constexpr (SPARSE) {
+      const int j = p.idx[(int64_t)bh * p.k_cap + u_begin + t];
+      if (j >= 0 && (int64_t)j * p.unit_tokens < seq_len) {
+        lo = j * p.unit_tokens;
+        hi = min(lo + p.unit_tokens, seq_len);
+      }
+    } else {
+      lo = (u_begin + t) * p.unit_tokens;
+      hi = min(lo + p.unit_tokens, seq_len);
+    }
+    unit_lo[t] = lo;
+    unit_hi[t] = hi;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nu * nsub_u; t += kThreads) {
+    const int u = t / nsub_u;
+    const int tok = unit_lo[u] + 16 * (t - u * nsub_u);
+    int pg = -1;
+    if (tok < unit_hi[u]) {
+      const int lp = tok / page_size;
+      if (!bt_row) {
+        pg = lp;
+      } else if (lp < kv.bt_cols) {
+        pg = bt_row[lp];
+      }
+      if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = -1;
+    }
+    sub_page[t] = pg;
+  }
+
+  // ---- query rows of this kv head, in the lane's dim slice
+  constexpr int QW = kBf16 ? DPL / 2 : DPL;  // bf16 pairs or floats
+  u32 qw[G][QW];
+  {
+    const int d0 = c16 * DPL;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
+      float qf[DPL];
+      if (p.q_f32) {
+        const float* qp = reinterpret_cast<const float*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) qf[e] = qp[e];
+      } else {
+        const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) qf[e] = __uint_as_float((u32)qp[e] << 16);
+      }
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) qw[g][e] = pack_bf16x2(qf[2 * e], qf[2 * e + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) qw[g][e] = __float_as_uint(qf[e]);
+      }
+    }
+  }
+  __syncthreads();
+
+  const char* kbase = reinterpret_cast<const char*>(kv.k) + (int64_t)h * kv.k_head_stride * KV::kBytes;
+  const char* vbase = reinterpret_cast<const char*>(kv.v) + (int64_t)h * kv.v_head_stride * KV::kBytes;
+  const int lane_off = c16 * DPL * KV::kBytes;
+
+  // Per-lane ownership of reduce-scattered scores: token step and query rows.
+  const int my_step = c16 >> 2;
+  int my_g[KG];
+#pragma unroll
+  for (int k = 0; k < KG; ++k) {
+    if constexpr (G == 8) my_g[k] = 2 * (c16 & 3) + k;
+    else if constexpr (G == 4) my_g[k] = c16 & 3;
+    else if constexpr (G == 2) my_g[k] = (c16 >> 1) & 1;
+    else my_g[k] = 0;
+  }
+  // For G < 4 several lanes hold copies of one score; only one copy counts in l.
+  const bool l_owner = (G >= 4) || ((c16 & (G == 2 ? 1 : 3)) == 0);
+
+  float m_run[KG], l_run[KG];
+#pragma unroll
+  for (int k = 0; k < KG; ++k) {
+    m_run[k] = kNegInf;
+    l_run[k] = 0.f;
+  }
+  float acc[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
+
+  // ---- subtile iterator over this wave's units (u = wave, wave + 4, ...)
+  struct Sub {
+    int u;   // local unit index; >= nu when exhausted
+    int s;   // subtile within the unit
+    int ts;  // first token
+    int hi;  // end of the unit's valid tokens
+    int pg;  // page id
+  };
+  auto seek = [&](int u, int s) -> Sub {
+    while (u < nu) {
+      const int lo = unit_lo[u], hi = unit_hi[u];
+      for (; lo + 16 * s < hi; ++s) {
+        const int pg = sub_page[u * nsub_u + s];
+        if (pg >= 0) return Sub{u, s, lo + 16 * s, hi, pg};
+      }
+      u += kWaves;
+      s = 0;
+    }
+    return Sub{nu, 0, 0, 0, -1};
+  };
+  auto next = [&](const Sub& c) -> Sub { return c.u < nu ? seek(c.u, c.s + 1) : c; };
+
+  auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
+    if (sb.u >= nu) return;
+    const int in_page = sb.ts % page_size;
+    const char* kp = kbase + ((int64_t)sb.pg * kv.k_page_stride + (int64_t)in_page * kv.k_token_stride) * KV::kBytes;
+    const char* vp = vbase + ((int64_t)sb.pg * kv.v_page_stride + (int64_t)in_page * kv.v_token_stride) * KV::kBytes;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // rows past the unit's end re-read the subtile's first row (always valid); their weights are zero
+      const int tl = (sb.ts + 4 * i + r < sb.hi) ? 4 * i + r : 0;
+      load_words<NWD>(kp + (int64_t)tl * kv.k_token_stride * KV::kBytes + lane_off, kb[i]);
+      load_words<NWD>(vp + (int64_t)tl * kv.v_token_stride * KV::kBytes + lane_off, vb[i]);
+    }
+  };
+
+  auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+    // ---------------- scores of the 16 tokens x G rows
+    float part[NV];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float a = 0.f;
+#pragma unroll
+          for (int w = 0; w < NWD; ++w)
+            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kb[i][w]), a, false);
+          part[i * G + g] = a;
+        }
+      } else {
+        float kf[DPL];
+        if constexpr (kFp8) {
+#pragma unroll
+          for (int w = 0; w < NWD; ++w) fp8x4_to_f32(kb[i][w], kf + 4 * w);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) kf[e] = __uint_as_float(kb[i][e]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), kf[e], a);
+          part[i * G + g] = a;
+        }
+      }
+    }
+    reduce_scatter16<NV>(part, lane);
+    float sc = p.scale_log2;
+    float vsc = 1.f;
+    if constexpr (kFp8) {
+      sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+      vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+    }
+    const bool valid = sb.ts + 4 * my_step + r < sb.hi;
+
+    // ---------------- online softmax, one update per subtile
+    float pw[KG], m_new[KG];
+    bool grow = false;
+#pragma unroll
+    for (int k = 0; k < KG; ++k) {
+      const float sv = valid ? part[k] * sc : kNegInf;
+      const float mt = fold_g<G, true>(sv);
+      m_new[k] = fmaxf(m_run[k], mt);
+      grow |= m_new[k] > m_run[k];
+      pw[k] = (sv == kNegInf) ? 0.f : exp2f(sv - m_new[k]);
+    }
+    if (__any(grow)) {
+      float alpha[KG];
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        alpha[k] = (m_new[k] == kNegInf) ? 1.f : exp2f(m_run[k] - m_new[k]);
+        l_run[k] *= alpha[k];
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float a = alpha_of_row<G>(alpha, g);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[g][e] *= a;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KG; ++k) {
+      m_run[k] = m_new[k];
+      l_run[k] += l_owner ? pw[k] : 0.f;
+    }
+
+    // ---------------- weighted values: weight of (token 4i + r, g) by row broadcast
+    float pb[4][G];
+    WeightBcast<G, 4 * G>::run(pw, pb);
+    if constexpr (kBf16) {
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const int i1 = 2 * pr, i2 = 2 * pr + 1;
+        u32 pp[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) pp[g] = pack_bf16x2(pb[i1][g], pb[i2][g]);
+#pragma unroll
+        for (int w = 0; w < NWD; ++w) {
+          const u32 lo = __builtin_amdgcn_perm(vb[i2][w], vb[i1][w], 0x05040100u);
+          const u32 hi = __builtin_amdgcn_perm(vb[i2][w], vb[i1][w], 0x07060302u);
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            acc[g][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(lo), acc[g][2 * w], false);
+            acc[g][2 * w + 1] =
+                __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(hi), acc[g][2 * w + 1], false);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float vf[DPL];
+        if constexpr (kFp8) {
+#pragma unroll
+          for (int w = 0; w < NWD; ++w) fp8x4_to_f32(vb[i][w], vf + 4 * w);
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) vf[e] = __uint_as_float(vb[i][e]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float wgt = pb[i][g] * vsc;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(wgt, vf[e], acc[g][e]);
+        }
+      }
+    }
+  };
+
+  // ---- software pipeline over a ring of NBUF register buffers: while subtile n
+  // is consumed, subtiles n+1 .. n+NBUF-1 are in flight
+  constexpr int NBUF = KV::kRing;
+  u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD];
+  Sub ring[NBUF];
+  ring[0] = seek(wave, 0);
+  issue(ring[0], kbuf[0], vbuf[0]);
+#pragma unroll
+  for (int k = 1; k < NBUF - 1; ++k) {
+    ring[k] = next(ring[k - 1]);
+    issue(ring[k], kbuf[k], vbuf[k]);
+  }
+  bool done = false;
+  while (!done) {
+#pragma unroll
+    for (int k = 0; k < NBUF; ++k) {
+      const int fk = (k + NBUF - 1) % NBUF;  // free buffer
+      const int pk = (k + NBUF - 2) % NBUF;  // most recently issued
+      if (ring[k].u >= nu) {
+        done = true;
+        break;
+      }
+      ring[fk] = next(ring[pk]);
+      issue(ring[fk], kbuf[fk], vbuf[fk]);
+      consume(ring[k], kbuf[k], vbuf[k]);
+    }
+  }
+
+  // ---- fold the wave: rows (xor 16, 32) for acc, g-sharing lanes for l
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      float v = acc[g][e];
+      v += shfl_xor_f(v, 16);
+      v += shfl_xor_f(v, 32);
+      acc[g][e] = v;
+    }
+#pragma unroll
+  for (int k = 0; k < KG; ++k) l_run[k] = fold_g<G, false>(l_run[k]);
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) wacc_lds[wave][g * D + c16 * DPL + e] = acc[g][e];
+  }
+  if (r == 0 && c16 < 4) {
+#pragma unroll
+    for (int k = 0; k < KG; ++k) {
+      wm_lds[wave][my_g[k]] = m_run[k];
+      wl_lds[wave][my_g[k]] = l_run[k];
+    }
+  }
+  __syncthreads();
+
+  // ---- fold the four waves: one (m, l, acc) per item, or the output when the item is alone
+  const int64_t pbase = (int64_t)bh * p.max_items + item;
+  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+    const int g = o / D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm_lds[w][g]);
+    float a = 0.f, l = 0.f;
+    if (M != kNegInf) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = wm_lds[w][g];
+        const float f = (mw == kNegInf) ? 0.f : exp2f(mw - M);
+        a += f * wacc_lds[w][o];
+        l += f * wl_lds[w][g];
+      }
+    }
+    if (!split) {
+      store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
+    } else {
+      p.part_acc[pbase * (G * D) + o] = a;
+      if (o % D == 0) {
+        p.part_ml[(pbase * G + g) * 2 + 0] = M;
+        p.part_ml[(pbase * G + g) * 2 + 1] = l;
+      }
+    }
+  }
+}
+
+// Split-K merge of the partials of every (sequence, kv head):
+// out = sum_c acc_c 2^(m_c - M) / max(sum_c l_c 2^(m_c - M), 1e-30), M = max_c m_c
+// (the reduce of CBT/legacy.py:765-794, in the log2 domain of the partials).
+// Every one of the n_slots slots was written (empty items wrote m = -inf), so no
+// load here depends on another.
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
+  const int bh = blockIdx.x;
+  const int b = bh / p.n_kv_heads;
+  const int h = bh - b * p.n_kv_heads;
+  const int64_t pbase = (int64_t)bh * p.max_items;
+  constexpr int kBatch = 8;  // slots whose loads are in flight together
+  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+    const int g = o / D;
+    float M = kNegInf, a = 0.f, l = 0.f;
+    for (int c0 = 0; c0 < n_slots; c0 += kBatch) {
+      float mc[kBatch], lc[kBatch], ac[kBatch];
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        const bool in = c0 + t < n_slots;
+        const int64_t slot = pbase + c0 + t;
+        mc[t] = in ? p.part_ml[(slot * G + g) * 2] : kNegInf;
+        lc[t] = in ? p.part_ml[(slot * G + g) * 2 + 1] : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        // an empty slot (m = -inf) never had its acc written
+        ac[t] = (mc[t] != kNegInf) ? p.part_acc[(pbase + c0 + t) * (G * D) + o] : 0.f;
+      }
+      float mb = kNegInf;
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) mb = fmaxf(mb, mc[t]);
+      const float m_new = fmaxf(M, mb);
+      if (m_new != kNegInf) {
+        const float fo = (M == kNegInf) ? 0.f : exp2f(M - m_new);
+        a *= fo;
+        l *= fo;
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+          if (mc[t] == kNegInf) continue;
+          const float f = exp2f(mc[t] - m_new);
+          a += f * ac[t];
+          l += f * lc[t];
+        }
+      }
+      M = m_new;
+    }
+    store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
+  }
+}
+
+// Per-instance launcher; returns IA_OK or an error code.
+template <int D, int G, typename KV, bool SPARSE>
+int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SPARSE>), grid, dim3(kThreads), 0, st, p);
+  int rc = check_launch("paged decode");
+  if (rc || grid.x == 1) return rc;
+  hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(grid.y * grid.z), dim3(kThreads), 0, st, p,
+                     (int)grid.x);
+  return check_launch("split-k merge");
+}
+
+// Resident workgroups of one instance on the current device (cached).
+template <int D, int G, typename KV, bool SPARSE>
+int resident_wgs() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SPARSE>), kThreads,
+            0) != hipSuccess)
+      return 0;
+    cached = std::max(1, cus * per_cu);
+  }
+  return cached;
+}
+
+// Dispatch by kv dtype for one (D, G): defined in paged_decode_{bf16,f32,fp8}.hip.
+int dispatch_bf16(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
+int dispatch_f32(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
+int dispatch_fp8(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
+
+}  // namespace ia

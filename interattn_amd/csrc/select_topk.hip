@@ -1,15 +1,19 @@
-// Top-k block selection for gfx950: block scorer + per-(sequence, kv head)
-// radix select in one launch.
+// Top-k block selection for gfx950: block scorer and per-(sequence, kv head)
+// radix select fused in one launch, one 1024-thread workgroup per (sequence,
+// kv head).  A whole score row stays inside one workgroup, so the launch needs
+// no cross-workgroup synchronisation (an agent-scope fence writes back the
+// XCD's L2 and costs far more than the work here).
 //
-//   grid = (score chunks, Hkv, batch), 256 threads.  Each workgroup scores
-//   kChunk blocks of one (sequence, kv head): score_j = (mean_g q_g) . k_bar_j
-//   / sqrt(D), one k_bar row per 16 lanes (4 rows per wave-wide load), DPP
-//   row sums.  Scores go to global memory; the last workgroup of the (sequence,
-//   kv head) -- device-scope counter -- selects:
+//   scoring: score_j = (mean_g q_g) . k_bar_j / sqrt(D); one k_bar row per 16
+//   lanes (4 rows per wave-wide load), 16 (bf16) or 8 (fp32) rows per lane in
+//   flight, DPP row sums;
+//   scores land in LDS (and in global memory when requested or too many).
+//   selection:
 //     * forced blocks: the first forced_first and last forced_last valid blocks;
 //     * the k_eff largest remaining scores by an MSB-first 8-bit radix select
-//       on order-preserving 32-bit keys (4 histogram passes in LDS), ties at
-//       the threshold taken in ascending block order;
+//       on order-preserving 32-bit keys (histograms in LDS), stopping as soon as
+//       the threshold bin is taken whole; ties at the threshold go to the
+//       lowest block indices;
 //     * an ordered compaction (wave ballots + LDS offsets) writes the chosen
 //       block ids in ascending order.
 //   The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
@@ -20,9 +24,9 @@ namespace ia {
 
 namespace {
 
-constexpr int kSelThreads = 256;
+constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
-constexpr int kChunk = 256;  // blocks scored per workgroup
+constexpr int kMaxLdsScores = 8192;
 
 struct SelectParams {
   const void* q;
@@ -35,10 +39,10 @@ struct SelectParams {
   int32_t* idx;
   int32_t k_cap;
   int32_t* n_sel;
-  float* scores;  // [batch*Hkv, nb_max]
-  u32* counters;  // [batch*Hkv]
+  float* scores;  // [batch*Hkv, nb_max] or null
   int32_t n_kv_heads;
-  float score_scale;  // 1 / (G * sqrt(D))
+  float score_scale;   // 1 / (G * sqrt(D))
+  int32_t lds_scores;  // score rows of up to this many blocks stay in LDS
 };
 
 __device__ __forceinline__ u32 order_key(float s) {
@@ -50,6 +54,7 @@ template <int D, int G, bool QF32, bool KBF16>
 __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(SelectParams p) {
   constexpr int DPL = D / 16;
   __shared__ u32 hist[256];
+  extern __shared__ float sc_lds[];  // p.lds_scores floats
   __shared__ int sh_int[8];
   __shared__ int wave_cnt[2][kSelWaves];
 
@@ -57,82 +62,96 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
   const int wave = threadIdx.x >> 6;
   const int c16 = lane & 15;
   const int r = lane >> 4;
-  const int chunk = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
   const int bh = b * p.n_kv_heads + h;
-
   const int seq_len = max(p.seq_lens[b], 0);
   const int nb = min((seq_len + p.block_size - 1) / p.block_size, p.nb_max);
-  const int n_chunks = max(1, (nb + kChunk - 1) / kChunk);
-  if (chunk >= n_chunks) return;
+  const bool in_lds = nb <= p.lds_scores;
+  float* sc_row = p.scores ? p.scores + (int64_t)bh * p.nb_max : nullptr;
 
-  // ---- mean query of the group, this lane's dims
-  float qm[DPL];
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) qm[e] = 0.f;
+  // ---- q rows (loaded first, summed after the first k_bar loads are in flight)
+  float qv[G][DPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
-      float v;
-      if constexpr (QF32) v = reinterpret_cast<const float*>(p.q)[row + e];
-      else v = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
-      qm[e] += v;
+      if constexpr (QF32) qv[g][e] = reinterpret_cast<const float*>(p.q)[row + e];
+      else qv[g][e] = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
     }
   }
+  float qm[DPL];
+  bool have_qm = false;
 
-  // ---- score this chunk: wave w handles rows j = chunk*kChunk + 4*(w + 4*step) + r
-  float* sc_row = p.scores + (int64_t)bh * p.nb_max;
-  const int j0 = chunk * kChunk;
-  const int j1 = min(nb, j0 + kChunk);
+  // ---- scores: in step t, wave w handles row base + 64 t + 4 w + r; NR steps in flight
   const char* kb = reinterpret_cast<const char*>(p.k_bar) +
                    ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * (KBF16 ? 2 : 4);
-  for (int base = j0 + 4 * wave; base < j1; base += 4 * kSelWaves) {
-    const int j = base + r;
-    float a = 0.f;
-    if (j < j1) {
-      const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * (KBF16 ? 2 : 4);
-      if constexpr (KBF16) {
-        u32 w[DPL / 2];
-        if constexpr (DPL == 8) {
-          const uint4 v = *reinterpret_cast<const uint4*>(rowp);
-          w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-        } else {
-          const uint2 v = *reinterpret_cast<const uint2*>(rowp);
-          w[0] = v.x; w[1] = v.y;
-        }
+  constexpr int EB = KBF16 ? 2 : 4;
+  constexpr int NWR = DPL * EB / 4;  // words per lane per row
+  constexpr int NR = KBF16 ? 16 : 8;
+  constexpr int kRowsPerStep = 4 * kSelWaves;
+  for (int base = 0; base < nb; base += NR * kRowsPerStep) {
+    u32 w[NR][NWR];
 #pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) {
-          a = fmaf(qm[2 * e], bf16_lo(w[e]), a);
-          a = fmaf(qm[2 * e + 1], bf16_hi(w[e]), a);
+    for (int t = 0; t < NR; ++t) {
+      const int j = base + kRowsPerStep * t + 4 * wave + r;
+      if (j < nb) {
+        const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * EB;
+        if constexpr (NWR >= 4) {
+#pragma unroll
+          for (int v4 = 0; v4 < NWR; v4 += 4) {
+            const uint4 x = reinterpret_cast<const uint4*>(rowp)[v4 / 4];
+            w[t][v4] = x.x; w[t][v4 + 1] = x.y; w[t][v4 + 2] = x.z; w[t][v4 + 3] = x.w;
+          }
+        } else {
+          const uint2 x = *reinterpret_cast<const uint2*>(rowp);
+          w[t][0] = x.x; w[t][1] = x.y;
         }
       } else {
-        const float* fp = reinterpret_cast<const float*>(rowp);
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], fp[e], a);
+        for (int e = 0; e < NWR; ++e) w[t][e] = 0u;
       }
     }
-    a = row16_sum(a);
-    if (c16 == 0 && j < j1) sc_row[j] = a * p.score_scale;
+    if (!have_qm) {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        float a = 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) a += qv[g][e];
+        qm[e] = a;
+      }
+      have_qm = true;
+    }
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      float a = 0.f;
+      if constexpr (KBF16) {
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) {
+          a = fmaf(qm[2 * e], bf16_lo(w[t][e]), a);
+          a = fmaf(qm[2 * e + 1], bf16_hi(w[t][e]), a);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], __uint_as_float(w[t][e]), a);
+      }
+      a = row16_sum(a) * p.score_scale;
+      const int j = base + kRowsPerStep * t + 4 * wave + r;
+      if (c16 == 0 && j < nb) {
+        if (in_lds) sc_lds[j] = a;
+        if (sc_row) sc_row[j] = a;
+      }
+    }
   }
   // blocks past this sequence's end read as -inf
-  if (chunk == n_chunks - 1) {
+  if (sc_row) {
     for (int j = nb + threadIdx.x; j < p.nb_max; j += kSelThreads) sc_row[j] = kNegInf;
   }
-
-  // ---- last workgroup of (b, h) selects
-  __threadfence();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const u32 prev = atomicAdd(&p.counters[bh], 1u);
-    sh_int[0] = (prev == (u32)(n_chunks - 1));
-  }
-  __syncthreads();
-  if (!sh_int[0]) return;
-  __threadfence();
+  auto key_at = [&](int j) -> u32 { return order_key(in_lds ? sc_lds[j] : sc_row[j]); };
 
+  // ---- selection rule
   const int ff = min(max(p.forced_first, 0), nb);
   const int fl_start = max(nb - max(p.forced_last, 0), 0);
   auto is_forced = [&](int j) { return j < ff || j >= fl_start; };
@@ -144,18 +163,19 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
   const int k_room = max(p.k_cap - n_forced, 0);
   k_eff = min(k_eff, k_room);
 
-  u32 thr = 0u;       // threshold key; candidates with key > thr are taken
-  int take_ties = 0;  // number of candidates with key == thr taken (lowest indices first)
-  bool take_all = k_eff >= n_cand;
+  u32 thr = 0u;       // threshold prefix; candidates with (key & thr_mask) > thr are taken
+  u32 thr_mask = 0u;
+  int take_ties = 0;  // candidates with (key & thr_mask) == thr taken, lowest indices first
+  const bool take_all = k_eff >= n_cand;
   if (!take_all && k_eff > 0) {
     u32 prefix = 0u, mask = 0u;
     int remaining = k_eff;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      hist[threadIdx.x] = 0u;
+      if (threadIdx.x < 256) hist[threadIdx.x] = 0u;
       __syncthreads();
       for (int j = threadIdx.x; j < nb; j += kSelThreads) {
         if (is_forced(j)) continue;
-        const u32 key = order_key(sc_row[j]);
+        const u32 key = key_at(j);
         if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
       __syncthreads();
@@ -168,8 +188,7 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
           c[t] = hist[255 - 4 * lane - t];
           tot += c[t];
         }
-        // inclusive scan over lanes (descending-bin order)
-        u32 inc = tot;
+        u32 inc = tot;  // inclusive scan over lanes (descending-bin order)
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
           const u32 o = __shfl_up(inc, off, 64);
@@ -182,8 +201,9 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             if (run + c[t] >= (u32)remaining) {
-              sh_int[1] = 255 - 4 * lane - t;     // digit
-              sh_int[2] = remaining - (int)run;   // still needed inside this bin
+              sh_int[1] = 255 - 4 * lane - t;    // digit
+              sh_int[2] = remaining - (int)run;  // still needed inside this bin
+              sh_int[3] = (int)c[t];             // candidates inside this bin
               break;
             }
             run += c[t];
@@ -193,11 +213,14 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
       __syncthreads();
       const u32 digit = (u32)sh_int[1];
       remaining = sh_int[2];
+      const int in_bin = sh_int[3];
       prefix |= digit << shift;
       mask |= 255u << shift;
       __syncthreads();
+      if (remaining == in_bin) break;  // the whole bin is taken: the threshold is exact
     }
     thr = prefix;
+    thr_mask = mask;
     take_ties = remaining;
   }
 
@@ -213,7 +236,7 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
         if (take_all) {
           above = true;
         } else if (k_eff > 0) {
-          const u32 key = order_key(sc_row[j]);
+          const u32 key = key_at(j) & thr_mask;
           above = key > thr;
           tie = key == thr;
         }
@@ -244,29 +267,23 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
     base_tie += tot_t;
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    p.n_sel[bh] = min(base_sel, p.k_cap);
-    p.counters[bh] = 0u;
-  }
+  if (threadIdx.x == 0) p.n_sel[bh] = min(base_sel, p.k_cap);
 }
-
-}  // namespace
-
-namespace {
 
 size_t select_ws_size(int batch, int hkv, int nb_max) {
   const size_t bh = (size_t)batch * hkv;
-  return align_up(bh * 4, 256) + bh * (size_t)std::max(nb_max, 1) * 4;
+  return bh * (size_t)std::max(nb_max, 1) * 4;
 }
 
 template <int D, int G>
 int launch_select(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipStream_t st) {
+  const size_t lds = (size_t)p.lds_scores * sizeof(float);
   if (qf32) {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, true>), grid, dim3(kSelThreads), 0, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, false>), grid, dim3(kSelThreads), 0, st, p);
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, true>), grid, dim3(kSelThreads), lds, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, false>), grid, dim3(kSelThreads), lds, st, p);
   } else {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, true>), grid, dim3(kSelThreads), 0, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, false>), grid, dim3(kSelThreads), 0, st, p);
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, true>), grid, dim3(kSelThreads), lds, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, false>), grid, dim3(kSelThreads), lds, st, p);
   }
   return check_launch("select_topk");
 }
@@ -282,9 +299,9 @@ size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t 
 
 int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
                    int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens,
-                   int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq,
-                   int32_t forced_first, int32_t forced_last, int32_t forced_in_k, int32_t* idx, int32_t k_cap,
-                   int32_t* n_sel, float* scores, void* workspace, size_t workspace_bytes, void* stream) {
+                   int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
+                   int32_t forced_last, int32_t forced_in_k, int32_t* idx, int32_t k_cap, int32_t* n_sel,
+                   float* scores, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace ia;
   if (!shape) return fail(IA_ERR_INVALID, "shape is null");
   if (shape->batch < 0 || shape->n_kv_heads <= 0 || shape->n_q_heads % shape->n_kv_heads != 0)
@@ -303,11 +320,9 @@ int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_ba
   if ((kbar_batch_stride * eb) % 16 || (kbar_head_stride * eb) % 16 || reinterpret_cast<uintptr_t>(k_bar) % 16)
     return fail(IA_ERR_INVALID, "k_bar rows must be 16-byte aligned");
   const size_t need = select_ws_size(shape->batch, shape->n_kv_heads, nb_max);
-  if (!workspace || workspace_bytes < need)
+  if (!scores && nb_max > kMaxLdsScores && (!workspace || workspace_bytes < need))
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
   if (shape->batch == 0) return IA_OK;
-  char* ws = reinterpret_cast<char*>(workspace);
-  const size_t bh = (size_t)shape->batch * shape->n_kv_heads;
   SelectParams p{};
   p.q = q;
   p.q_batch_stride = shape->q_batch_stride;
@@ -326,12 +341,12 @@ int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_ba
   p.idx = idx;
   p.k_cap = k_cap;
   p.n_sel = n_sel;
-  p.counters = reinterpret_cast<u32*>(ws);
-  p.scores = scores ? scores : reinterpret_cast<float*>(ws + align_up(bh * 4, 256));
+  // scores go to global memory when asked for, or when a row does not fit in LDS
+  p.scores = scores ? scores : (nb_max > kMaxLdsScores ? reinterpret_cast<float*>(workspace) : nullptr);
   p.n_kv_heads = shape->n_kv_heads;
   p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
-  const int n_chunks = std::max(1, (nb_max + kChunk - 1) / kChunk);
-  dim3 grid(n_chunks, shape->n_kv_heads, shape->batch);
+  p.lds_scores = nb_max <= kMaxLdsScores ? nb_max : 0;
+  dim3 grid(shape->n_kv_heads, shape->batch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool qf32 = shape->q_dtype == IA_F32;
   const bool kbf16 = k_bar_dtype == IA_BF16;

@@ -11,8 +11,8 @@ float32.
 Every function launches on the current torch stream and never synchronises, except
 where a docstring says otherwise.  Scratch space lives in a caller-owned
 ``workspace`` dict (the reference's ``_workspace_empty`` convention,
-CBT/core.py:558-570): tensors are created on first use (zero-filled), reused while
-the shapes match, and the kernels leave their counters zeroed for the next call.
+CBT/core.py:558-570): tensors are created on first use and reused while the shapes
+match, so steady-state calls allocate nothing (and can be captured in a graph).
 """
 
 import math
@@ -47,7 +47,7 @@ def workspace_tensor(workspace, key, shape, *, device, dtype, zero=False):
     """Reuse ``workspace[key]`` when shape/dtype/device match, else (re)create it.
 
     Mirrors ``_workspace_empty`` (CBT/core.py:558-570); ``zero=True`` zero-fills a new
-    tensor (counters must start at zero; the kernels re-zero them after use)."""
+    tensor."""
     shape = tuple(int(s) for s in shape)
     make = torch.zeros if zero else torch.empty
     if workspace is None:

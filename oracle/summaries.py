@@ -57,6 +57,6 @@ def build_block_summaries(k, v, block, k_bar_dtype="f32", v_bar_dtype="f32"):
         "k_max": k_max.astype(np.float32),
         "k_min": k_min.astype(np.float32),
         "v_norm_max": v_norm_max.astype(np.float32),
-        "v_norm_all": v_norm_max.max(axis=-1).astype(np.float32),
+        "v_norm_all": (v_norm_max.max(axis=-1) if nb else np.full(hkv, -np.inf)).astype(np.float32),
         "block_valid_counts": counts,
     }

@@ -208,3 +208,26 @@ def selection_finalize(stats, prefix, group, eps, term1_mass_exp=False):
     mean = cond.reshape(hkv, group, nb).sum(axis=1) / group
     sel = (mean > eps) & active[None]
     return np.repeat(sel, group, axis=0), z
+
+
+def condition_stats(selected, counts, prompt_len, suffix_len):
+    """Restates ``_condition_stats`` (CBT/core.py:1441-1456) for one query position.
+
+    ``selected [Hkv, G, 1, nb]`` bool, ``counts [nb]``.  Returns the reference's keys:
+    rows, clusters, selected_clusters, selected_tokens, hybrid_tokens, total_available.
+    """
+    hkv, g, nq, nb = selected.shape
+    counts = np.asarray(counts).astype(np.int64)
+    exists = counts > 0
+    sel = np.asarray(selected, dtype=bool)
+    selected_tokens = int((sel.astype(np.int64) * counts[None, None, None]).sum())
+    cluster_active = (~sel) & exists[None, None, None]
+    rows = hkv * g * nq
+    return {
+        "rows": rows,
+        "clusters": int(exists.sum()) * hkv * g,
+        "selected_clusters": int(sel.sum()),
+        "selected_tokens": selected_tokens,
+        "hybrid_tokens": selected_tokens + int(cluster_active.sum()) + max(int(suffix_len), 0) * hkv * g,
+        "total_available": (int(prompt_len) + max(int(suffix_len), 0)) * rows,
+    }

@@ -162,6 +162,95 @@ IA_API int ia_paged_decode(const ia_decode_shape* shape, const void* q, const ia
                     const int32_t* seq_lens, int32_t max_seq_len, float scale, void* out,
                     int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Per-block summaries consumed by the condition (eps-threshold) rule: arrays
+ * [batch, Hkv, nb, D] (k_bar, k_max, k_min, v_bar; contiguous), v_norm_max
+ * [batch, Hkv, nb] and v_norm_all [batch, Hkv] float32, counts [batch, nb]
+ * int32 (valid tokens per block; 0 = no block).  block_size = tokens per block.
+ * This is the prefix dict of _build_prompt_blocks (CBT/core.py:449-500) with a
+ * batch dimension.
+ */
+typedef struct ia_block_summaries {
+  const void* k_bar;
+  const void* k_max;
+  const void* k_min;
+  const void* v_bar;
+  int32_t k_bar_dtype, bounds_dtype, v_bar_dtype; /* IA_F32 or IA_BF16 */
+  const float* v_norm_max;
+  const float* v_norm_all;
+  const int32_t* counts;
+  int32_t nb;
+  int32_t block_size;
+} ia_block_summaries;
+
+/*
+ * The exact suffix (generated tokens kept outside the blocks, CBT/core.py:1316-
+ * 1324): token t of batch entry b, kv head h at k + b*k_batch_stride +
+ * h*k_head_stride + t*k_token_stride (elements, same dtype as the prompt K/V).
+ * len is device memory (entry b, or entry 0 for all when len_stride == 0) so a
+ * captured decode step can advance it (CBT/page_attention.py:256-259); cap bounds it.
+ */
+typedef struct ia_suffix_kv {
+  const void* k;
+  const void* v;
+  int64_t k_batch_stride, k_head_stride, k_token_stride;
+  int64_t v_batch_stride, v_head_stride, v_token_stride;
+  const int32_t* len;
+  int32_t len_stride;
+  int32_t cap;
+} ia_suffix_kv;
+
+/*
+ * Selection statistics of the condition rule: replaces
+ * _run_condition_block_selection_stats / _condition_block_selection_stats_kernel
+ * (CBT/core.py:573-698, :747-814) and, when globals != NULL, the reduce kernel
+ * (CBT/core.py:817-847).  Outputs s, delta [batch, rows, nb], partial
+ * [batch, 4, rows, ceil(nb/16)] = (z_m, z_l, c_m, c_l) per 16-block chunk,
+ * globals [batch, 4, rows].
+ */
+IA_API int ia_condition_selection_stats(const ia_decode_shape* shape, const void* q,
+                                        const ia_block_summaries* sm, int32_t term1_mass_exp,
+                                        float* s, float* delta, float* partial, float* globals,
+                                        void* stream);
+
+/*
+ * The eps threshold of the condition rule: replaces
+ * _condition_block_selection_finalize_kernel (CBT/core.py:850-905).  selected
+ * [batch, rows, nb] uint8 (the group decision broadcast to the group's rows),
+ * z [batch, rows, nb] float32 (may be NULL).
+ */
+IA_API int ia_condition_select(const ia_decode_shape* shape, const ia_block_summaries* sm,
+                               const float* s, const float* delta, const float* globals, float eps,
+                               int32_t term1_mass_exp, uint8_t* selected, float* z, void* stream);
+
+/*
+ * Fused condition-block decode: statistics, routing, representatives of the
+ * unselected blocks, the selected blocks' tokens and the exact suffix in one
+ * online softmax.  Replaces _condition_block_decode_output_fused_triton
+ * (CBT/core.py:1035-1155).  selected (optional) receives [batch, rows, nb].
+ * out: [batch, n_q_heads, D].
+ */
+IA_API size_t ia_condition_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
+                                          int32_t head_dim, int32_t nb, int32_t suffix_cap);
+IA_API int ia_condition_decode(const ia_decode_shape* shape, const void* q,
+                               const ia_block_summaries* sm, const ia_paged_kv* prompt,
+                               const ia_suffix_kv* suffix, float eps, int32_t term1_mass_exp,
+                               uint8_t* selected, float scale, void* out, int32_t out_dtype,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Hybrid decode with an external per-(batch, kv head) block mask [batch, Hkv, nb]
+ * uint8: representatives recomputed as q.k_bar/sqrt(D) + log(count), q and k_bar
+ * rounded to bfloat16 for bfloat16 caches.
+ * Replaces fixed_mask_hybrid_attention (CBG/real_attention_benchmark/fixed_mask.py:
+ * 250-348).  Workspace as for ia_condition_decode.
+ */
+IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
+                                const ia_block_summaries* sm, const uint8_t* mask,
+                                const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float scale,
+                                void* out, int32_t out_dtype, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* Number of split-K items per (b, h) the two decode entry points use for the
  * given workload; size the decode workspace with it.  max_seq_len must bound
  * every seq_lens[b] passed to ia_paged_decode (tokens past it are not read). */

@@ -65,6 +65,39 @@ class DecodeShape(ctypes.Structure):
     ]
 
 
+class BlockSummaries(ctypes.Structure):
+    _fields_ = [
+        ("k_bar", ctypes.c_void_p),
+        ("k_max", ctypes.c_void_p),
+        ("k_min", ctypes.c_void_p),
+        ("v_bar", ctypes.c_void_p),
+        ("k_bar_dtype", ctypes.c_int32),
+        ("bounds_dtype", ctypes.c_int32),
+        ("v_bar_dtype", ctypes.c_int32),
+        ("v_norm_max", ctypes.c_void_p),
+        ("v_norm_all", ctypes.c_void_p),
+        ("counts", ctypes.c_void_p),
+        ("nb", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+    ]
+
+
+class SuffixKV(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_batch_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64),
+        ("k_token_stride", ctypes.c_int64),
+        ("v_batch_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64),
+        ("v_token_stride", ctypes.c_int64),
+        ("len", ctypes.c_void_p),
+        ("len_stride", ctypes.c_int32),
+        ("cap", ctypes.c_int32),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -96,6 +129,20 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, _I32, _F, _P, _I32, _P, _SZ, _P],
     ),
+    "ia_condition_selection_stats": (
+        ctypes.c_int, [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _I32, _P, _P, _P, _P, _P]),
+    "ia_condition_select": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), ctypes.POINTER(BlockSummaries), _P, _P, _P, _F, _I32, _P, _P, _P]),
+    "ia_condition_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "ia_condition_decode": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), ctypes.POINTER(PagedKV),
+         ctypes.POINTER(SuffixKV), _F, _I32, _P, _F, _P, _I32, _P, _SZ, _P]),
+    "ia_fixed_mask_decode": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _P, ctypes.POINTER(PagedKV),
+         ctypes.POINTER(SuffixKV), _F, _P, _I32, _P, _SZ, _P]),
     "ia_sparse_max_items": (_I32, [_I32, _I32, _I32]),
     "ia_dense_max_items": (_I32, [_I32, _I32, _I32]),
 }

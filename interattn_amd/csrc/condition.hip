@@ -1,0 +1,814 @@
+// Condition-block (eps-threshold) routing for gfx950: the reference's own
+// selection rule, next to the top-k rule of select_topk.hip.
+//
+//   ia_condition_block_selection_stats  (CBT/core.py:747-814)
+//     grid = (ceil(n_chunks / 4), Hkv, batch), 256 threads; wave w owns chunk
+//     c = 4*blockIdx.x + w of 16 blocks (the reference's _SELECT_CHUNK).  Per
+//     block and query row: s = q.k_bar/sqrt(D), the range bound upper/lower
+//     from the sign of q against k_max/k_min, delta = max(|upper-s|, |lower-s|),
+//     z = s + log(max(count,1)), zc = z + log cosh(delta) (or z + delta for the
+//     term1-mass-exp variant); one k_bar/k_max/k_min row per 16 lanes, DPP row
+//     sums.  Writes s, delta and the chunk's (max, sum-exp) partials of z and zc.
+//   ia_condition_block_selection_reduce  (CBT/core.py:821-847)
+//     log-sum-exp merge of the chunk partials into per-row globals.
+//   ia_condition_block_selection_select  (CBT/core.py:854-905)
+//     term1 = 2 B_all e^(z-c_m)/c_l (cosh delta - 1), term2 = 2 b_c e^(z-z_m)/z_l
+//     tanh(delta/2); selected = mean_g(term1 + term2) > eps (and the block exists).
+//   ia_condition_block_route  (CBT/page_attention.py:104-204)
+//     one workgroup per 256 blocks of a (sequence, kv head): reduces the chunk
+//     partials inline, thresholds, writes the selected flags, compacts the
+//     selected block ids (wave ballots) for the finalize, and computes the
+//     representative softmax partial of the unselected blocks: logit z, value
+//     v_bar, weight beta, fp32 sums.  For bfloat16 caches value and weight are
+//     rounded to bfloat16 (the reference's cast points, CBT/page_attention.py:
+//     194-201); float32 caches stay float32 throughout.  In fixed-mask mode the
+//     selection comes from a caller mask and the logit is recomputed as
+//     q.k_bar/sqrt(D) + log(count), with q and k_bar rounded to bfloat16 for
+//     bfloat16 caches (CBG/real_attention_benchmark/fixed_mask.py:86-107).
+//   The selected blocks and the exact suffix are then streamed by the paged
+//   finalize (kSrcLists) and merged with the representative partials.
+#include <algorithm>
+#include <string>
+
+#include "paged_decode_kernel.hpp"
+
+namespace ia {
+namespace {
+
+constexpr int kChunk16 = 16;  // blocks per selection-stats partial
+
+struct CondParams {
+  const void* q;
+  int64_t q_batch_stride, q_row_stride;
+  int32_t q_f32;
+  const void* k_bar;
+  const void* k_max;
+  const void* k_min;
+  const void* v_bar;
+  const float* v_norm_max;  // [batch, Hkv, nb]
+  const float* v_norm_all;  // [batch, Hkv]
+  const int32_t* counts;    // [batch, nb]
+  int32_t nb, n_kv_heads, n_chunks;
+  float scale;  // 1/sqrt(D)
+  int32_t mass_exp;
+  float eps;
+  float* s;        // [batch, rows, nb]
+  float* delta;    // [batch, rows, nb]
+  float* partial;  // [batch, 4, rows, n_chunks]
+  float* globals;  // [batch, 4, rows]
+  uint8_t* selected;  // [batch, rows, nb] (optional)
+  float* z_out;       // [batch, rows, nb] (optional)
+  int32_t* rc_counts;  // [batch*Hkv, n_rc]
+  int32_t* rc_lists;   // [batch*Hkv, n_rc, kRouteChunk]
+  int32_t n_rc;
+  float* rep_ml;   // [batch*Hkv, n_rc, G, 2]
+  float* rep_acc;  // [batch*Hkv, n_rc, G, D]
+  const uint8_t* mask;  // fixed-mask mode: [batch, Hkv, nb]
+  int32_t rep_bf16;     // bfloat16 caches: representative operands rounded to bfloat16
+};
+
+__device__ __forceinline__ float round_if(float x, bool rnd) {
+  return rnd ? __uint_as_float((u32)f32_to_bf16_bits(x) << 16) : x;
+}
+
+template <bool BF16>
+__device__ __forceinline__ void load_row(const void* base, int64_t off, float* out, int n) {
+  if constexpr (BF16) {
+    const unsigned short* p = reinterpret_cast<const unsigned short*>(base) + off;
+    if (n == 8) {
+      const uint4 w = *reinterpret_cast<const uint4*>(p);
+      out[0] = bf16_lo(w.x); out[1] = bf16_hi(w.x); out[2] = bf16_lo(w.y); out[3] = bf16_hi(w.y);
+      out[4] = bf16_lo(w.z); out[5] = bf16_hi(w.z); out[6] = bf16_lo(w.w); out[7] = bf16_hi(w.w);
+    } else {
+      const uint2 w = *reinterpret_cast<const uint2*>(p);
+      out[0] = bf16_lo(w.x); out[1] = bf16_hi(w.x); out[2] = bf16_lo(w.y); out[3] = bf16_hi(w.y);
+    }
+  } else {
+    const float* p = reinterpret_cast<const float*>(base) + off;
+    for (int e = 0; e < n; e += 4) {
+      const float4 w = *reinterpret_cast<const float4*>(p + e);
+      out[e] = w.x; out[e + 1] = w.y; out[e + 2] = w.z; out[e + 3] = w.w;
+    }
+  }
+}
+
+__device__ __forceinline__ float q_elem(const CondParams& p, int64_t off) {
+  return p.q_f32 ? reinterpret_cast<const float*>(p.q)[off]
+                 : __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[off] << 16);
+}
+
+// log cosh(d) = |d| + log1p(e^{-2|d|}) - log 2, without overflow
+__device__ __forceinline__ float log_cosh(float d) {
+  const float a = fabsf(d);
+  return a + log1pf(__expf(-2.f * a)) - 0.69314718055994531f;
+}
+
+// cosh(d) - 1 = 2 sinh^2(d/2), without cancellation for small d
+__device__ __forceinline__ float cosh_m1(float d) {
+  const float sh = sinhf(0.5f * d);
+  return 2.f * sh * sh;
+}
+
+// ---------------------------------------------------------------- selection stats
+
+template <int D, int G, bool KBH, bool BDH>
+__global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondParams p) {
+  constexpr int DPL = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const int chunk = blockIdx.x * 4 + wave;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  if (chunk >= p.n_chunks) return;  // whole wave; no workgroup barrier below
+
+  float qf[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e)
+      qf[g][e] = q_elem(p, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL + e);
+
+  const int64_t vbase = ((int64_t)b * p.n_kv_heads + h) * p.nb;
+  float zs[4], zcs[4];
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int j = chunk * kChunk16 + 4 * step + r;
+    const bool inb = j < p.nb;
+    const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
+    const bool active = cnt > 0;
+    float kb[DPL], kh[DPL], kl[DPL];
+    if (active) {
+      load_row<KBH>(p.k_bar, (vbase + j) * D + c16 * DPL, kb, DPL);
+      load_row<BDH>(p.k_max, (vbase + j) * D + c16 * DPL, kh, DPL);
+      load_row<BDH>(p.k_min, (vbase + j) * D + c16 * DPL, kl, DPL);
+    } else {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) kb[e] = kh[e] = kl[e] = 0.f;
+    }
+    float ps[G], pu[G], pl[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float a = 0.f, u = 0.f, l = 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const float qv = qf[g][e];
+        a = fmaf(qv, kb[e], a);
+        u = fmaf(qv, qv >= 0.f ? kh[e] : kl[e], u);
+        l = fmaf(qv, qv >= 0.f ? kl[e] : kh[e], l);
+      }
+      ps[g] = row16_sum(a);
+      pu[g] = row16_sum(u);
+      pl[g] = row16_sum(l);
+    }
+    // lane c16 < G finishes row g = c16
+    float sv = 0.f, uv = 0.f, lv = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (g == c16) {
+        sv = ps[g];
+        uv = pu[g];
+        lv = pl[g];
+      }
+    sv *= p.scale;
+    uv *= p.scale;
+    lv *= p.scale;
+    const float dl = fmaxf(fabsf(uv - sv), fabsf(lv - sv));
+    const float z = active ? sv + __logf((float)max(cnt, 1)) : kNegInf;
+    zs[step] = z;
+    zcs[step] = active ? (p.mass_exp ? z + dl : z + log_cosh(dl)) : kNegInf;
+    if (c16 < G && inb) {
+      const int64_t o = ((int64_t)b * (p.n_kv_heads * G) + h * G + c16) * p.nb + j;
+      p.s[o] = active ? sv : 0.f;
+      p.delta[o] = active ? dl : 0.f;
+    }
+  }
+  // chunk partials over the 16 blocks: 4 steps in-lane, 4 rows across lanes
+  float mz = fmaxf(fmaxf(zs[0], zs[1]), fmaxf(zs[2], zs[3]));
+  float mc = fmaxf(fmaxf(zcs[0], zcs[1]), fmaxf(zcs[2], zcs[3]));
+  mz = fmaxf(mz, shfl_xor_f(mz, 16));
+  mz = fmaxf(mz, shfl_xor_f(mz, 32));
+  mc = fmaxf(mc, shfl_xor_f(mc, 16));
+  mc = fmaxf(mc, shfl_xor_f(mc, 32));
+  float lz = 0.f, lc = 0.f;
+  if (mz != kNegInf) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) lz += (zs[t] == kNegInf) ? 0.f : __expf(zs[t] - mz);
+  }
+  if (mc != kNegInf) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) lc += (zcs[t] == kNegInf) ? 0.f : __expf(zcs[t] - mc);
+  }
+  lz += shfl_xor_f(lz, 16);
+  lz += shfl_xor_f(lz, 32);
+  lc += shfl_xor_f(lc, 16);
+  lc += shfl_xor_f(lc, 32);
+  if (r == 0 && c16 < G) {
+    const int rows = p.n_kv_heads * G;
+    const int64_t base = (int64_t)b * 4 * rows * p.n_chunks + (int64_t)(h * G + c16) * p.n_chunks + chunk;
+    const int64_t plane = (int64_t)rows * p.n_chunks;
+    p.partial[base] = mz;
+    p.partial[base + plane] = lz;
+    p.partial[base + 2 * plane] = mc;
+    p.partial[base + 3 * plane] = lc;
+  }
+}
+
+__global__ __launch_bounds__(256) void ia_condition_block_selection_reduce(CondParams p, int rows, int batch) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= rows * batch) return;
+  const int b = t / rows;
+  const int row = t - b * rows;
+  const int64_t plane = (int64_t)rows * p.n_chunks;
+  const float* base = p.partial + (int64_t)b * 4 * plane + (int64_t)row * p.n_chunks;
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const float* m = base + (2 * v) * plane;
+    const float* l = base + (2 * v + 1) * plane;
+    float M = kNegInf;
+    for (int c = 0; c < p.n_chunks; ++c) M = fmaxf(M, m[c]);
+    float L = 0.f;
+    if (M != kNegInf)
+      for (int c = 0; c < p.n_chunks; ++c) L += (m[c] == kNegInf) ? 0.f : l[c] * __expf(m[c] - M);
+    p.globals[(int64_t)b * 4 * rows + (2 * v) * rows + row] = M;
+    p.globals[(int64_t)b * 4 * rows + (2 * v + 1) * rows + row] = L;
+  }
+}
+
+// condition of one (row, block); returns term1 + term2 (0 for an empty block)
+__device__ __forceinline__ float condition_value(float s, float dl, float z, float zm, float zl, float cm, float cl,
+                                                 float b_c, float b_all, bool mass_exp) {
+  float term1, tanh_half;
+  if (mass_exp) {
+    const float en = __expf(-dl);
+    tanh_half = (1.f - en) / (1.f + en);
+    term1 = 2.f * b_all * __expf(z + dl - cm) / cl;
+  } else {
+    tanh_half = tanhf(0.5f * dl);
+    term1 = 2.f * b_all * __expf(z - cm) * cosh_m1(dl) / cl;
+  }
+  const float term2 = 2.f * b_c * __expf(z - zm) * tanh_half / zl;
+  (void)s;
+  return term1 + term2;
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void ia_condition_block_selection_select(CondParams p) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  if (j >= p.nb) return;
+  const int rows = p.n_kv_heads * G;
+  const int cnt = p.counts[(int64_t)b * p.nb + j];
+  const bool active = cnt > 0;
+  const float lc = __logf((float)max(cnt, 1));
+  const float b_c = active ? p.v_norm_max[((int64_t)b * p.n_kv_heads + h) * p.nb + j] : 0.f;
+  const float b_all = p.v_norm_all[(int64_t)b * p.n_kv_heads + h];
+  float z[G], mean = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int row = h * G + g;
+    const int64_t o = ((int64_t)b * rows + row) * p.nb + j;
+    const float s = active ? p.s[o] : 0.f;
+    const float dl = active ? p.delta[o] : 0.f;
+    z[g] = active ? s + lc : kNegInf;
+    const float* gl = p.globals + (int64_t)b * 4 * rows;
+    if (active)
+      mean += condition_value(s, dl, z[g], gl[row], gl[rows + row], gl[2 * rows + row], gl[3 * rows + row], b_c,
+                              b_all, p.mass_exp);
+  }
+  mean /= (float)G;
+  const uint8_t sel = (active && mean > p.eps) ? 1 : 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t o = ((int64_t)b * rows + h * G + g) * p.nb + j;
+    if (p.selected) p.selected[o] = sel;
+    if (p.z_out) p.z_out[o] = z[g];
+  }
+}
+
+// ---------------------------------------------------------------- route + representatives
+
+template <int D, int G, bool VBH, bool KBH, bool MASK>
+__global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
+  constexpr int DPL = D / 16;
+  __shared__ float z_lds[G][kRouteChunk];
+  __shared__ float red[8][G];
+  __shared__ float glob[4][G];
+  __shared__ int wcnt[4];
+  __shared__ float wacc[4][G * D];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const int rc = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int bh = b * p.n_kv_heads + h;
+  const int rows = p.n_kv_heads * G;
+  const int j = rc * kRouteChunk + threadIdx.x;
+  const bool inb = j < p.nb;
+  const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
+  const bool active = cnt > 0;
+  const float logc = __logf((float)max(cnt, 1));
+
+  // ---- per-row globals from the stats partials (condition mode)
+  if constexpr (!MASK) {
+    const int64_t plane = (int64_t)rows * p.n_chunks;
+    for (int g = 0; g < G; ++g) {
+      const float* base = p.partial + (int64_t)b * 4 * plane + (int64_t)(h * G + g) * p.n_chunks;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const float* m = base + (2 * v) * plane;
+        const float* l = base + (2 * v + 1) * plane;
+        float M = kNegInf;
+        for (int c = threadIdx.x; c < p.n_chunks; c += 256) M = fmaxf(M, m[c]);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        if (lane == 0) red[wave][0] = M;
+        __syncthreads();
+        M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
+        __syncthreads();
+        float L = 0.f;
+        if (M != kNegInf)
+          for (int c = threadIdx.x; c < p.n_chunks; c += 256) L += (m[c] == kNegInf) ? 0.f : l[c] * __expf(m[c] - M);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+        if (lane == 0) red[wave][0] = L;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          glob[2 * v][g] = M;
+          glob[2 * v + 1][g] = red[0][0] + red[1][0] + red[2][0] + red[3][0];
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  // ---- routing of this thread's block
+  bool sel = false;
+  if constexpr (MASK) {
+    sel = active && p.mask[((int64_t)b * p.n_kv_heads + h) * p.nb + j] != 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) z_lds[g][threadIdx.x] = kNegInf;  // logits computed below
+  } else {
+    const float b_c = active ? p.v_norm_max[((int64_t)b * p.n_kv_heads + h) * p.nb + j] : 0.f;
+    const float b_all = p.v_norm_all[(int64_t)b * p.n_kv_heads + h];
+    float z[G], mean = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t o = ((int64_t)b * rows + h * G + g) * p.nb + j;
+      const float s = active ? p.s[o] : 0.f;
+      const float dl = active ? p.delta[o] : 0.f;
+      z[g] = active ? s + logc : kNegInf;
+      if (active) mean += condition_value(s, dl, z[g], glob[0][g], glob[1][g], glob[2][g], glob[3][g], b_c, b_all,
+                                          p.mass_exp);
+    }
+    mean /= (float)G;
+    sel = active && mean > p.eps;
+#pragma unroll
+    for (int g = 0; g < G; ++g) z_lds[g][threadIdx.x] = (active && !sel) ? z[g] : kNegInf;
+  }
+  if (p.selected && inb) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) p.selected[((int64_t)b * rows + h * G + g) * p.nb + j] = sel ? 1 : 0;
+  }
+
+  // ---- compaction of the selected block ids, ascending
+  const unsigned long long ballot = __ballot(sel);
+  if (lane == 0) wcnt[wave] = __popcll(ballot);
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; ++w) off += wcnt[w];
+  if (sel) p.rc_lists[((int64_t)bh * p.n_rc + rc) * kRouteChunk + off + __popcll(ballot & ((1ull << lane) - 1ull))] = j;
+  if (threadIdx.x == 0) p.rc_counts[(int64_t)bh * p.n_rc + rc] = wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+
+  // ---- fixed-mask mode: representative logits q.k_bar/sqrt(D) + log(count)
+  if constexpr (MASK) {
+    float qb[G][DPL];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const float qv = q_elem(p, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL + e);
+        qb[g][e] = round_if(qv, p.rep_bf16);
+      }
+    __syncthreads();  // z_lds initialised
+    for (int t = 0; t < kRouteChunk / 16; ++t) {
+      const int jl = 16 * t + 4 * wave + r;  // local block row
+      const int jj = rc * kRouteChunk + jl;
+      const bool in2 = jj < p.nb;
+      const int cnt2 = in2 ? p.counts[(int64_t)b * p.nb + jj] : 0;
+      const bool rep = cnt2 > 0 && p.mask[((int64_t)b * p.n_kv_heads + h) * p.nb + jj] == 0;
+      float kb[DPL];
+      if (rep) {
+        load_row<KBH>(p.k_bar, (((int64_t)b * p.n_kv_heads + h) * p.nb + jj) * D + c16 * DPL, kb, DPL);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) kb[e] = round_if(kb[e], p.rep_bf16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) kb[e] = 0.f;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float a = 0.f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) a = fmaf(qb[g][e], kb[e], a);
+        a = row16_sum(a);
+        if (c16 == 0 && rep) z_lds[g][jl] = a * p.scale + __logf((float)cnt2);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- representative softmax partial: max, weights, weighted v_bar
+  float mg[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = z_lds[g][threadIdx.x];
+#pragma unroll
+    for (int o2 = 32; o2 >= 1; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+    if (lane == 0) red[wave][g] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) mg[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float zv = z_lds[g][threadIdx.x];
+    const float beta = (zv == kNegInf) ? 0.f : __expf(zv - mg[g]);
+    z_lds[g][threadIdx.x] = beta;  // reuse as the fp32 weight
+    float l = beta;
+#pragma unroll
+    for (int o2 = 32; o2 >= 1; o2 >>= 1) l += __shfl_xor(l, o2, 64);
+    if (lane == 0) red[4 + wave][g] = l;
+  }
+  __syncthreads();
+
+  float acc[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
+  for (int t = 0; t < kRouteChunk / 16; ++t) {
+    const int jl = 16 * t + 4 * wave + r;
+    const int jj = rc * kRouteChunk + jl;
+    float bw[G];
+    bool any = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      bw[g] = z_lds[g][jl];
+      any |= bw[g] != 0.f;
+    }
+    if (!any || jj >= p.nb) continue;
+    float vb[DPL];
+    load_row<VBH>(p.v_bar, (((int64_t)b * p.n_kv_heads + h) * p.nb + jj) * D + c16 * DPL, vb, DPL);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float wq = round_if(bw[g], p.rep_bf16);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e)
+        acc[g][e] = fmaf(wq, round_if(vb[e], p.rep_bf16), acc[g][e]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      float v = acc[g][e];
+      v += shfl_xor_f(v, 16);
+      v += shfl_xor_f(v, 32);
+      if (r == 0) wacc[wave][g * D + c16 * DPL + e] = v;
+    }
+  __syncthreads();
+  const int64_t slot = (int64_t)bh * p.n_rc + rc;
+  for (int o = threadIdx.x; o < G * D; o += 256) {
+    const int g = o / D;
+    p.rep_acc[slot * (G * D) + o] = wacc[0][o] + wacc[1][o] + wacc[2][o] + wacc[3][o];
+    if (o % D == 0) {
+      // partials use the finalize's log2 domain
+      p.rep_ml[(slot * G + g) * 2 + 0] = mg[g] == kNegInf ? kNegInf : mg[g] * kLog2e;
+      p.rep_ml[(slot * G + g) * 2 + 1] = red[4][g] + red[5][g] + red[6][g] + red[7][g];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- host
+
+int check_summaries(const ia_block_summaries* sm, bool need_bounds, bool need_v) {
+  if (!sm || !sm->k_bar || !sm->counts) return fail(IA_ERR_INVALID, "summaries need k_bar and counts");
+  if (need_bounds && (!sm->k_max || !sm->k_min)) return fail(IA_ERR_INVALID, "summaries need k_max and k_min");
+  if (need_v && (!sm->v_bar || !sm->v_norm_max || !sm->v_norm_all))
+    return fail(IA_ERR_INVALID, "summaries need v_bar, v_norm_max and v_norm_all");
+  const int32_t dts[3] = {sm->k_bar_dtype, sm->bounds_dtype, sm->v_bar_dtype};
+  for (int32_t dt : dts)
+    if (dt != IA_F32 && dt != IA_BF16) return fail(IA_ERR_INVALID, "summary dtypes must be IA_F32 or IA_BF16");
+  if (sm->nb < 0 || sm->block_size <= 0 || sm->block_size % 16)
+    return fail(IA_ERR_INVALID, "nb must be >= 0 and block_size a positive multiple of 16");
+  const void* ptrs[4] = {sm->k_bar, sm->k_max, sm->k_min, sm->v_bar};
+  for (const void* q : ptrs)
+    if (reinterpret_cast<uintptr_t>(q) % 16) return fail(IA_ERR_INVALID, "summary arrays must be 16-byte aligned");
+  return IA_OK;
+}
+
+CondParams cond_params(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm) {
+  CondParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.q_f32 = shape->q_dtype == IA_F32;
+  p.k_bar = sm->k_bar;
+  p.k_max = sm->k_max;
+  p.k_min = sm->k_min;
+  p.v_bar = sm->v_bar;
+  p.v_norm_max = sm->v_norm_max;
+  p.v_norm_all = sm->v_norm_all;
+  p.counts = sm->counts;
+  p.nb = sm->nb;
+  p.n_kv_heads = shape->n_kv_heads;
+  p.n_chunks = std::max(1, (sm->nb + kChunk16 - 1) / kChunk16);
+  p.scale = 1.0f / std::sqrt((float)shape->head_dim);
+  return p;
+}
+
+template <int D, int G>
+void launch_stats(const CondParams& p, bool kbh, bool bdh, int batch, hipStream_t st) {
+  dim3 grid((p.n_chunks + 3) / 4, p.n_kv_heads, batch);
+  if (kbh) {
+    if (bdh) hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, true, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, true, false>), grid, dim3(256), 0, st, p);
+  } else {
+    if (bdh) hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, false, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, false, false>), grid, dim3(256), 0, st, p);
+  }
+}
+
+template <int D, int G, bool MASK>
+void launch_route(const CondParams& p, bool vbh, bool kbh, int batch, hipStream_t st) {
+  dim3 grid(p.n_rc, p.n_kv_heads, batch);
+  if (vbh) {
+    if (kbh) hipLaunchKernelGGL((ia_condition_block_route<D, G, true, true, MASK>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_route<D, G, true, false, MASK>), grid, dim3(256), 0, st, p);
+  } else {
+    if (kbh) hipLaunchKernelGGL((ia_condition_block_route<D, G, false, true, MASK>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_route<D, G, false, false, MASK>), grid, dim3(256), 0, st, p);
+  }
+}
+
+#define IA_DG_SWITCH(D, G, CALL)                                 \
+  do {                                                           \
+    if (D == 128 && G == 4) { constexpr int DD = 128, GG = 4; CALL; } \
+    else if (D == 128 && G == 8) { constexpr int DD = 128, GG = 8; CALL; } \
+    else if (D == 128 && G == 2) { constexpr int DD = 128, GG = 2; CALL; } \
+    else if (D == 128 && G == 1) { constexpr int DD = 128, GG = 1; CALL; } \
+    else if (D == 64 && G == 4) { constexpr int DD = 64, GG = 4; CALL; } \
+    else if (D == 64 && G == 8) { constexpr int DD = 64, GG = 8; CALL; } \
+    else if (D == 64 && G == 2) { constexpr int DD = 64, GG = 2; CALL; } \
+    else if (D == 64 && G == 1) { constexpr int DD = 64, GG = 1; CALL; } \
+    else return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination"); \
+  } while (0)
+
+struct CondWs {
+  float* s;
+  float* delta;
+  float* partial;
+  int32_t* rc_counts;
+  int32_t* rc_lists;
+  float* rep_ml;
+  float* rep_acc;
+  char* decode;
+  size_t decode_bytes;
+  size_t total;
+};
+
+CondWs cond_ws_layout(int batch, int hkv, int g, int d, int nb, int max_items, char* base) {
+  CondWs w{};
+  const size_t rows = (size_t)hkv * g;
+  const size_t bh = (size_t)batch * hkv;
+  const size_t n16 = std::max(1, (nb + kChunk16 - 1) / kChunk16);
+  const size_t nrc = std::max(1, (nb + kRouteChunk - 1) / kRouteChunk);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes, 256);
+    return base ? base + o : nullptr;
+  };
+  w.s = reinterpret_cast<float*>(take((size_t)batch * rows * std::max(nb, 1) * 4));
+  w.delta = reinterpret_cast<float*>(take((size_t)batch * rows * std::max(nb, 1) * 4));
+  w.partial = reinterpret_cast<float*>(take((size_t)batch * 4 * rows * n16 * 4));
+  w.rc_counts = reinterpret_cast<int32_t*>(take(bh * nrc * 4));
+  w.rc_lists = reinterpret_cast<int32_t*>(take(bh * nrc * kRouteChunk * 4));
+  w.rep_ml = reinterpret_cast<float*>(take(bh * nrc * g * 2 * 4));
+  w.rep_acc = reinterpret_cast<float*>(take(bh * nrc * g * d * 4));
+  w.decode_bytes = decode_ws_size(batch, hkv, g, d, max_items);
+  w.decode = take(w.decode_bytes);
+  w.total = off;
+  return w;
+}
+
+int64_t cond_units_max(int nb, int32_t sfx_cap) {
+  return (int64_t)nb + (std::max(sfx_cap, 0) + kDenseTile - 1) / kDenseTile;
+}
+
+int run_condition(bool mask_mode, const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                  const uint8_t* mask, const ia_paged_kv* prompt, const ia_suffix_kv* sfx, float eps,
+                  int32_t mass_exp, uint8_t* selected, float scale, void* out, int32_t out_dtype, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  rc = check_summaries(sm, !mask_mode, true);
+  if (rc) return rc;
+  rc = check_kv(prompt, shape->head_dim);
+  if (rc) return rc;
+  if (prompt->dtype == IA_FP8_E4M3) return fail(IA_ERR_UNSUPPORTED, "condition-mode decode takes f32 or bf16 K/V");
+  if (mask_mode && !mask) return fail(IA_ERR_INVALID, "fixed-mask decode needs a mask");
+  if (!q || !out) return fail(IA_ERR_INVALID, "q and out must be non-null");
+  if (out_dtype != IA_F32 && out_dtype != IA_BF16) return fail(IA_ERR_INVALID, "out dtype must be IA_F32 or IA_BF16");
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(IA_ERR_INVALID, "scale must be positive and finite");
+  if (sfx && sfx->cap > 0) {
+    if (!sfx->k || !sfx->v || !sfx->len) return fail(IA_ERR_INVALID, "suffix needs k, v and a device length");
+    const int eb = prompt->dtype == IA_F32 ? 4 : 2;
+    const int64_t st6[6] = {sfx->k_batch_stride, sfx->k_head_stride, sfx->k_token_stride,
+                            sfx->v_batch_stride, sfx->v_head_stride, sfx->v_token_stride};
+    for (int64_t s6 : st6)
+      if (s6 < 0 || (s6 * eb) % 16) return fail(IA_ERR_INVALID, "suffix strides must be 16-byte multiples");
+    if ((reinterpret_cast<uintptr_t>(sfx->k) | reinterpret_cast<uintptr_t>(sfx->v)) % 16)
+      return fail(IA_ERR_INVALID, "suffix pointers must be 16-byte aligned");
+  }
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  const int nb = sm->nb;
+  const int n_rc = std::max(1, (nb + kRouteChunk - 1) / kRouteChunk);
+  if (n_rc > kMaxRouteChunks) return fail(IA_ERR_UNSUPPORTED, "too many blocks per sequence for condition mode");
+  const int32_t sfx_cap = (sfx && sfx->cap > 0) ? sfx->cap : 0;
+  const int64_t units_max = cond_units_max(nb, sfx_cap);
+  const int cap_items = units_cap_items(units_max);
+  const CondWs need = cond_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb, cap_items, nullptr);
+  if (!workspace || workspace_bytes < need.total)
+    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need.total) + " bytes");
+  if (shape->batch == 0) return IA_OK;
+  const CondWs ws = cond_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb, cap_items,
+                                   reinterpret_cast<char*>(workspace));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+
+  CondParams cp = cond_params(shape, q, sm);
+  cp.mass_exp = mass_exp;
+  cp.eps = eps;
+  cp.s = ws.s;
+  cp.delta = ws.delta;
+  cp.partial = ws.partial;
+  cp.selected = selected;
+  cp.rc_counts = ws.rc_counts;
+  cp.rc_lists = ws.rc_lists;
+  cp.n_rc = n_rc;
+  cp.rep_ml = ws.rep_ml;
+  cp.rep_acc = ws.rep_acc;
+  cp.mask = mask;
+  cp.rep_bf16 = prompt->dtype == IA_BF16;
+  const bool kbh = sm->k_bar_dtype == IA_BF16, bdh = sm->bounds_dtype == IA_BF16, vbh = sm->v_bar_dtype == IA_BF16;
+  if (nb > 0) {
+    if (!mask_mode) {
+      IA_DG_SWITCH(D, G, (launch_stats<DD, GG>(cp, kbh, bdh, shape->batch, st)));
+      rc = check_launch("condition stats");
+      if (rc) return rc;
+      IA_DG_SWITCH(D, G, (launch_route<DD, GG, false>(cp, vbh, kbh, shape->batch, st)));
+    } else {
+      IA_DG_SWITCH(D, G, (launch_route<DD, GG, true>(cp, vbh, kbh, shape->batch, st)));
+    }
+    rc = check_launch("condition route");
+    if (rc) return rc;
+  }
+
+  DecodeParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.kv = *prompt;
+  p.n_kv_heads = shape->n_kv_heads;
+  p.unit_tokens = sm->block_size;
+  p.scale_log2 = scale * kLog2e;
+  p.q_f32 = shape->q_dtype == IA_F32;
+  p.out_f32 = out_dtype == IA_F32;
+  p.out = out;
+  p.rc_counts = ws.rc_counts;
+  p.rc_lists = ws.rc_lists;
+  p.n_rc = nb > 0 ? n_rc : 0;
+  p.blk_counts = sm->counts;
+  p.nb_max = nb;
+  if (sfx_cap > 0) {
+    p.sfx_k = sfx->k;
+    p.sfx_v = sfx->v;
+    p.sfx_k_batch_stride = sfx->k_batch_stride;
+    p.sfx_k_head_stride = sfx->k_head_stride;
+    p.sfx_k_token_stride = sfx->k_token_stride;
+    p.sfx_v_batch_stride = sfx->v_batch_stride;
+    p.sfx_v_head_stride = sfx->v_head_stride;
+    p.sfx_v_token_stride = sfx->v_token_stride;
+    p.sfx_len = sfx->len;
+    p.sfx_len_stride = sfx->len_stride;
+    p.sfx_cap = sfx_cap;
+  }
+  p.rep_ml = nb > 0 ? ws.rep_ml : nullptr;
+  p.rep_acc = ws.rep_acc;
+  p.max_items = cap_items;
+  p.part_ml = reinterpret_cast<float*>(ws.decode);
+  p.part_acc = reinterpret_cast<float*>(ws.decode + align_up((size_t)shape->batch * shape->n_kv_heads * cap_items * G * 2 * 4, 256));
+  const int nsub_u = (std::max(sm->block_size, kDenseTile) + 15) / 16;
+  int items = 1;
+  rc = decode_items(p, prompt->dtype, D, G, kSrcLists, (int64_t)shape->batch * shape->n_kv_heads, units_max, nsub_u,
+                    cap_items, st, &items);
+  if (rc) return rc;
+  return dispatch_decode(p, prompt->dtype, D, G, kSrcLists, dim3(items, shape->n_kv_heads, shape->batch), st,
+                         nullptr);
+}
+
+}  // namespace
+}  // namespace ia
+
+extern "C" {
+
+size_t ia_condition_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim, int32_t nb,
+                                   int32_t suffix_cap) {
+  const int cap_items = ia::units_cap_items(ia::cond_units_max(nb, suffix_cap));
+  return ia::cond_ws_layout(batch, n_kv_heads, group, head_dim, nb, cap_items, nullptr).total;
+}
+
+int ia_condition_selection_stats(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                                 int32_t term1_mass_exp, float* s, float* delta, float* partial, float* globals,
+                                 void* stream) {
+  using namespace ia;
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  rc = check_summaries(sm, true, false);
+  if (rc) return rc;
+  if (!q || !s || !delta || !partial) return fail(IA_ERR_INVALID, "null pointer argument");
+  if (shape->batch == 0 || sm->nb == 0) return IA_OK;
+  CondParams cp = cond_params(shape, q, sm);
+  cp.mass_exp = term1_mass_exp;
+  cp.s = s;
+  cp.delta = delta;
+  cp.partial = partial;
+  cp.globals = globals;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  const bool kbh = sm->k_bar_dtype == IA_BF16, bdh = sm->bounds_dtype == IA_BF16;
+  IA_DG_SWITCH(D, G, (launch_stats<DD, GG>(cp, kbh, bdh, shape->batch, st)));
+  rc = check_launch("condition stats");
+  if (rc || !globals) return rc;
+  const int rows = shape->n_q_heads;
+  hipLaunchKernelGGL(ia_condition_block_selection_reduce, dim3((rows * shape->batch + 255) / 256), dim3(256), 0, st,
+                     cp, rows, shape->batch);
+  return check_launch("condition reduce");
+}
+
+int ia_condition_select(const ia_decode_shape* shape, const ia_block_summaries* sm, const float* s,
+                        const float* delta, const float* globals, float eps, int32_t term1_mass_exp,
+                        uint8_t* selected, float* z, void* stream) {
+  using namespace ia;
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  rc = check_summaries(sm, false, true);
+  if (rc) return rc;
+  if (!s || !delta || !globals || !selected) return fail(IA_ERR_INVALID, "null pointer argument");
+  if (shape->batch == 0 || sm->nb == 0) return IA_OK;
+  CondParams cp = cond_params(shape, nullptr, sm);
+  cp.mass_exp = term1_mass_exp;
+  cp.eps = eps;
+  cp.s = const_cast<float*>(s);
+  cp.delta = const_cast<float*>(delta);
+  cp.globals = const_cast<float*>(globals);
+  cp.selected = selected;
+  cp.z_out = z;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 grid((sm->nb + 255) / 256, shape->n_kv_heads, shape->batch);
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  switch (G) {
+    case 1: hipLaunchKernelGGL(ia_condition_block_selection_select<1>, grid, dim3(256), 0, st, cp); break;
+    case 2: hipLaunchKernelGGL(ia_condition_block_selection_select<2>, grid, dim3(256), 0, st, cp); break;
+    case 4: hipLaunchKernelGGL(ia_condition_block_selection_select<4>, grid, dim3(256), 0, st, cp); break;
+    case 8: hipLaunchKernelGGL(ia_condition_block_selection_select<8>, grid, dim3(256), 0, st, cp); break;
+    default: return fail(IA_ERR_UNSUPPORTED, "GQA group size");
+  }
+  return check_launch("condition select");
+}
+
+int ia_condition_decode(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                        const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float eps, int32_t term1_mass_exp,
+                        uint8_t* selected, float scale, void* out, int32_t out_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return ia::run_condition(false, shape, q, sm, nullptr, prompt, suffix, eps, term1_mass_exp, selected, scale, out,
+                           out_dtype, workspace, workspace_bytes, stream);
+}
+
+int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                         const uint8_t* mask, const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float scale,
+                         void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return ia::run_condition(true, shape, q, sm, mask, prompt, suffix, 0.f, 0, nullptr, scale, out, out_dtype,
+                           workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -6,10 +6,6 @@
 #include "paged_decode_kernel.hpp"
 
 namespace ia {
-namespace {
-
-// Upper bound of split-K items per (sequence, kv head); sizes the partials.
-constexpr int kMaxItemsPerBh = 64;
 
 int units_cap_items(int64_t units) { return (int)std::max<int64_t>(1, std::min<int64_t>(units, kMaxItemsPerBh)); }
 
@@ -55,16 +51,38 @@ int check_shape(const ia_decode_shape* s) {
   return IA_OK;
 }
 
-int dispatch(const DecodeParams& p, int kv_dtype, int d, int g, bool sparse, dim3 grid, hipStream_t st,
-             int* resident) {
-  if (kv_dtype == IA_BF16) return dispatch_bf16(p, d, g, sparse, grid, st, resident);
+int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, dim3 grid, hipStream_t st,
+                    int* resident) {
+  if (kv_dtype == IA_BF16) return dispatch_bf16(p, d, g, src, grid, st, resident);
   if (kv_dtype == IA_F32) {
     if (!p.q_f32) return fail(IA_ERR_UNSUPPORTED, "fp32 kv needs fp32 q");
-    return dispatch_f32(p, d, g, sparse, grid, st, resident);
+    return dispatch_f32(p, d, g, src, grid, st, resident);
   }
   if (p.q_f32) return fail(IA_ERR_UNSUPPORTED, "fp8 kv needs bf16 q");
-  return dispatch_fp8(p, d, g, sparse, grid, st, resident);
+  return dispatch_fp8(p, d, g, src, grid, st, resident);
 }
+
+int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
+                 int nsub_u, int cap_items, hipStream_t st, int* items_out) {
+  // about one resident round of workgroups over all (sequence, kv head)
+  int resident = 0;
+  int rc = dispatch_decode(p, kv_dtype, d, g, src, dim3(1), st, &resident);
+  if (rc) return rc;
+  if (resident <= 0) resident = 1024;
+  int items = (int)std::max<int64_t>(1, resident / std::max<int64_t>(bh, 1));
+  items = std::min(items, cap_items);
+  // the item prologue stages unit ranges and page ids in LDS: bound the units per item
+  const int upi_lds = std::min(kMaxUnitsPerItem, kMaxSubsPerItem / std::max(nsub_u, 1));
+  if (upi_lds < 1) return fail(IA_ERR_UNSUPPORTED, "block_size too large for one work item");
+  const int64_t need = (units_max + upi_lds - 1) / upi_lds;
+  if (need > cap_items)
+    return fail(IA_ERR_UNSUPPORTED, "sequence too long for one launch: " + std::to_string(units_max) + " units");
+  items = (int)std::max<int64_t>(items, need);
+  *items_out = std::max(items, 1);
+  return IA_OK;
+}
+
+namespace {
 
 int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
                const int32_t* seq_lens, int32_t block_size, const int32_t* idx, int32_t k_cap, const int32_t* n_sel,
@@ -110,30 +128,18 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   p.k_cap = k_cap;
   p.unit_tokens = unit_tokens;
   p.n_kv_heads = shape->n_kv_heads;
+  p.sfx_len_stride = 0;
   p.scale_log2 = scale * kLog2e;
   p.q_f32 = shape->q_dtype == IA_F32;
   p.out_f32 = out_dtype == IA_F32;
   p.out = out;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 
-  // Split-K sizing: about one resident round of workgroups over all (sequence, kv head).
-  int resident = 0;
-  rc = dispatch(p, kv->dtype, D, G, sparse, dim3(1), st, &resident);
-  if (rc) return rc;
-  if (resident <= 0) resident = 1024;
   const int64_t bh = (int64_t)shape->batch * shape->n_kv_heads;
-  int items = (int)std::max<int64_t>(1, resident / std::max<int64_t>(bh, 1));
-  items = std::min(items, cap_items);
-  int upi = (int)std::max<int64_t>(1, (units_max + items - 1) / items);
-  // the item prologue stages unit ranges and page ids in LDS
-  const int nsub_u = (unit_tokens + 15) / 16;
-  const int upi_lds = std::min(kMaxUnitsPerItem, kMaxSubsPerItem / nsub_u);
-  if (upi_lds < 1) return fail(IA_ERR_UNSUPPORTED, "block_size too large for one work item");
-  upi = std::min(upi, upi_lds);
-  items = (int)std::max<int64_t>(1, (units_max + upi - 1) / upi);
-  if (items > cap_items)
-    return fail(IA_ERR_UNSUPPORTED, "sequence too long for one launch: " + std::to_string(units_max) + " units");
-  p.upi = upi;
+  const int src = sparse ? kSrcTopk : kSrcDense;
+  int items = 1;
+  rc = decode_items(p, kv->dtype, D, G, src, bh, units_max, (unit_tokens + 15) / 16, cap_items, st, &items);
+  if (rc) return rc;
   p.max_items = cap_items;  // stride of the partials; items per (b, h) never exceed it
 
   char* ws = reinterpret_cast<char*>(workspace);
@@ -143,7 +149,7 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
     p.part_acc = reinterpret_cast<float*>(ws + align_up(nbh * cap_items * G * 2 * 4, 256));
   }
   dim3 grid(items, shape->n_kv_heads, shape->batch);
-  return dispatch(p, kv->dtype, D, G, sparse, grid, st, nullptr);
+  return dispatch_decode(p, kv->dtype, D, G, src, grid, st, nullptr);
 }
 
 }  // namespace

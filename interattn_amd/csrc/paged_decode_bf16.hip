@@ -4,16 +4,27 @@
 
 namespace ia {
 
-int dispatch_bf16(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident) {
-#define IA_CASE(DD, GG)                                                             \
-  if (d == DD && g == GG) {                                                         \
-    if (sparse) {                                                                   \
-      if (resident) return *resident = resident_wgs<DD, GG, KvBf16, true>(), IA_OK;   \
-      return launch_paged_finalize<DD, GG, KvBf16, true>(p, grid, st);                \
-    }                                                                               \
-    if (resident) return *resident = resident_wgs<DD, GG, KvBf16, false>(), IA_OK;    \
-    return launch_paged_finalize<DD, GG, KvBf16, false>(p, grid, st);                 \
+namespace {
+template <int D, int G>
+int run_bf16(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* resident) {
+  switch (src) {
+    case kSrcTopk:
+      if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcTopk>(), IA_OK;
+      return launch_paged_finalize<D, G, KvBf16, kSrcTopk>(p, grid, st);
+    case kSrcDense:
+      if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcDense>(), IA_OK;
+      return launch_paged_finalize<D, G, KvBf16, kSrcDense>(p, grid, st);
+    case kSrcLists:
+      if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcLists>(), IA_OK;
+      return launch_paged_finalize<D, G, KvBf16, kSrcLists>(p, grid, st);
   }
+  return fail(IA_ERR_UNSUPPORTED, "unit source");
+}
+}  // namespace
+
+int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident) {
+#define IA_CASE(DD, GG) \
+  if (d == DD && g == GG) return run_bf16<DD, GG>(p, src, grid, st, resident);
   IA_CASE(128, 4) IA_CASE(128, 8) IA_CASE(128, 2) IA_CASE(128, 1)
   IA_CASE(64, 4) IA_CASE(64, 8) IA_CASE(64, 2) IA_CASE(64, 1)
 #undef IA_CASE

@@ -71,17 +71,42 @@ __device__ __forceinline__ void load_words(const char* p, u32* w) {
   }
 }
 
+// Where a finalize launch takes its units from.
+constexpr int kSrcTopk = 0;   // idx[b, h, 0:n_sel[b, h]] blocks of unit_tokens tokens
+constexpr int kSrcDense = 1;  // every 128-token tile of [0, seq_len)
+constexpr int kSrcLists = 2;  // route-chunk lists of selected blocks, then the exact suffix
+
+constexpr int kRouteChunk = 256;      // blocks per route workgroup (condition mode)
+constexpr int kMaxRouteChunks = 256;  // route chunks per (sequence, kv head)
+constexpr int kNoPage = -1;
+constexpr int kSfxPage = -2;          // subtile of the contiguous suffix source
+
 struct DecodeParams {
   const void* q;
   int64_t q_batch_stride, q_row_stride;
   ia_paged_kv kv;
   const int32_t* seq_lens;
-  const int32_t* idx;  // sparse only
+  const int32_t* idx;  // kSrcTopk
   const int32_t* n_sel;
   int32_t k_cap;
-  int32_t unit_tokens;  // tokens per unit: block_size (sparse) or the dense tile
-  int32_t upi;          // units per item
-  int32_t max_items;
+  int32_t unit_tokens;  // tokens per unit: block_size (blocks) or the dense tile
+  int32_t max_items;    // stride of the item partials per (b, h)
+  // kSrcLists: selected blocks per route chunk, valid tokens per block, suffix
+  const int32_t* rc_counts;   // [batch*Hkv, n_rc]
+  const int32_t* rc_lists;    // [batch*Hkv, n_rc, kRouteChunk]
+  int32_t n_rc;
+  const int32_t* blk_counts;  // [batch, nb_max]
+  int32_t nb_max;
+  const void* sfx_k;
+  const void* sfx_v;
+  int64_t sfx_k_batch_stride, sfx_k_head_stride, sfx_k_token_stride;
+  int64_t sfx_v_batch_stride, sfx_v_head_stride, sfx_v_token_stride;
+  const int32_t* sfx_len;     // device: suffix length (entry b, or entry 0 when sfx_len_stride == 0)
+  int32_t sfx_len_stride;
+  int32_t sfx_cap;            // host bound on the suffix length
+  // representative partials folded by the merge (condition mode)
+  const float* rep_ml;        // [batch*Hkv, n_rc, G, 2]
+  const float* rep_acc;       // [batch*Hkv, n_rc, G, D]
   int32_t n_kv_heads;
   float scale_log2;  // softmax scale * log2(e)
   int32_t q_f32;     // q is fp32 (else bf16)
@@ -180,7 +205,7 @@ struct WeightBcast<G, 0> {
   __device__ __forceinline__ static void run(const float*, float (*)[G]) {}
 };
 
-template <int D, int G, typename KV, bool SPARSE>
+template <int D, int G, typename KV, int SRC>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
   constexpr int NWD = DPL * KV::kBytes / 4;
@@ -193,6 +218,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
   __shared__ int sub_page[kMaxSubsPerItem];
+  __shared__ int rc_prefix[SRC == kSrcLists ? kMaxRouteChunks + 1 : 1];
   __shared__ float wacc_lds[kWaves][G * D];
   __shared__ float wm_lds[kWaves][G];
   __shared__ float wl_lds[kWaves][G];
@@ -206,15 +232,39 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   const int b = blockIdx.z;
   const int bh = b * p.n_kv_heads + h;
 
-  const int seq_len = max(p.seq_lens[b], 0);
-  int n_units;
-  if constexpr (SPARSE) {
+  const int seq_len = (SRC == kSrcLists) ? 0 : max(p.seq_lens[b], 0);
+  int n_units, n_blk_units = 0, sfx_len = 0;
+  if constexpr (SRC == kSrcTopk) {
     n_units = min(max(p.n_sel[bh], 0), p.k_cap);
-  } else {
+  } else if constexpr (SRC == kSrcDense) {
     n_units = (seq_len + p.unit_tokens - 1) / p.unit_tokens;
+  } else {
+    // selected blocks of every route chunk (exclusive prefix in LDS), then the suffix tiles
+    if (wave == 0) {
+      int run = 0;
+      for (int c0 = 0; c0 < p.n_rc; c0 += 64) {
+        const int c = c0 + lane;
+        const int v = c < p.n_rc ? max(p.rc_counts[(int64_t)bh * p.n_rc + c], 0) : 0;
+        int inc = v;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int o = __shfl_up(inc, off, 64);
+          if (lane >= off) inc += o;
+        }
+        if (c < p.n_rc) rc_prefix[c] = run + inc - v;
+        run += __shfl(inc, 63, 64);
+      }
+      if (lane == 0) rc_prefix[p.n_rc] = run;
+    }
+    __syncthreads();
+    n_blk_units = rc_prefix[p.n_rc];
+    sfx_len = p.sfx_len ? min(max(p.sfx_len[(int64_t)b * p.sfx_len_stride], 0), p.sfx_cap) : 0;
+    n_units = n_blk_units + (sfx_len + kDenseTile - 1) / kDenseTile;
   }
-  const int n_items = max(1, min(p.max_items, (n_units + p.upi - 1) / p.upi));
-  const bool split = gridDim.x > 1;  // partials + merge kernel, else direct output
+  // units are spread evenly over the row's items
+  const int upi = max(1, (n_units + (int)gridDim.x - 1) / (int)gridDim.x);
+  const int n_items = max(1, (n_units + upi - 1) / upi);
+  const bool split = gridDim.x > 1 || p.rep_ml != nullptr;  // partials + merge kernel
   if (item >= n_items) {
     // an empty slot: the merge reads every slot of the grid row
     if (threadIdx.x < G) {
@@ -228,39 +278,66 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   const ia_paged_kv& kv = p.kv;
   const int page_size = kv.page_size;
   const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
-  const int u_begin = item * p.upi;
-  const int nu = max(0, min(n_units, u_begin + p.upi) - u_begin);
-  const int nsub_u = (p.unit_tokens + 15) / 16;
+  const int u_begin = item * upi;
+  const int nu = max(0, min(n_units, u_begin + upi) - u_begin);
+  const int nsub_u = ((SRC == kSrcLists ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
 
   // ---- prologue: token ranges of this item's units, then one page id per subtile
   for (int t = threadIdx.x; t < nu; t += kThreads) {
-    int lo = 0, hi = 0;
-    if constexpr (SPARSE) {
-      const int j = p.idx[(int64_t)bh * p.k_cap + u_begin + t];
+    const int u = u_begin + t;
+    int lo = 0, hi = 0, sfx = 0;
+    if constexpr (SRC == kSrcTopk) {
+      const int j = p.idx[(int64_t)bh * p.k_cap + u];
       if (j >= 0 && (int64_t)j * p.unit_tokens < seq_len) {
         lo = j * p.unit_tokens;
         hi = min(lo + p.unit_tokens, seq_len);
       }
-    } else {
-      lo = (u_begin + t) * p.unit_tokens;
+    } else if constexpr (SRC == kSrcDense) {
+      lo = u * p.unit_tokens;
       hi = min(lo + p.unit_tokens, seq_len);
+    } else {
+      if (u < n_blk_units) {
+        int lo_c = 0, hi_c = p.n_rc - 1;  // last chunk whose prefix <= u
+        while (lo_c < hi_c) {
+          const int mid = (lo_c + hi_c + 1) >> 1;
+          if (rc_prefix[mid] <= u) lo_c = mid;
+          else hi_c = mid - 1;
+        }
+        const int j = p.rc_lists[((int64_t)bh * p.n_rc + lo_c) * kRouteChunk + (u - rc_prefix[lo_c])];
+        if (j >= 0 && j < p.nb_max) {
+          lo = j * p.unit_tokens;
+          hi = lo + max(0, min(p.blk_counts[(int64_t)b * p.nb_max + j], p.unit_tokens));
+        }
+      } else {
+        lo = (u - n_blk_units) * kDenseTile;
+        hi = min(lo + kDenseTile, sfx_len);
+        sfx = 1;
+      }
     }
     unit_lo[t] = lo;
-    unit_hi[t] = hi;
+    unit_hi[t] = sfx ? -hi - 1 : hi;  // suffix units carry a negative end
   }
   __syncthreads();
   for (int t = threadIdx.x; t < nu * nsub_u; t += kThreads) {
     const int u = t / nsub_u;
-    const int tok = unit_lo[u] + 16 * (t - u * nsub_u);
-    int pg = -1;
-    if (tok < unit_hi[u]) {
-      const int lp = tok / page_size;
-      if (!bt_row) {
-        pg = lp;
-      } else if (lp < kv.bt_cols) {
-        pg = bt_row[lp];
+    const int lo = unit_lo[u];
+    const int hi_raw = unit_hi[u];
+    const bool sfx = hi_raw < 0;
+    const int hi = sfx ? -hi_raw - 1 : hi_raw;
+    const int tok = lo + 16 * (t - u * nsub_u);
+    int pg = kNoPage;
+    if (tok < hi) {
+      if (sfx) {
+        pg = kSfxPage;
+      } else {
+        const int lp = tok / page_size;
+        if (!bt_row) {
+          pg = lp;
+        } else if (lp < kv.bt_cols) {
+          pg = bt_row[lp];
+        }
+        if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = kNoPage;
       }
-      if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = -1;
     }
     sub_page[t] = pg;
   }
@@ -333,10 +410,12 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   };
   auto seek = [&](int u, int s) -> Sub {
     while (u < nu) {
-      const int lo = unit_lo[u], hi = unit_hi[u];
+      const int lo = unit_lo[u];
+      int hi = unit_hi[u];
+      if (hi < 0) hi = -hi - 1;  // suffix unit
       for (; lo + 16 * s < hi; ++s) {
         const int pg = sub_page[u * nsub_u + s];
-        if (pg >= 0) return Sub{u, s, lo + 16 * s, hi, pg};
+        if (pg != kNoPage) return Sub{u, s, lo + 16 * s, hi, pg};
       }
       u += kWaves;
       s = 0;
@@ -347,15 +426,29 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 
   auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
     if (sb.u >= nu) return;
-    const int in_page = sb.ts % page_size;
-    const char* kp = kbase + ((int64_t)sb.pg * kv.k_page_stride + (int64_t)in_page * kv.k_token_stride) * KV::kBytes;
-    const char* vp = vbase + ((int64_t)sb.pg * kv.v_page_stride + (int64_t)in_page * kv.v_token_stride) * KV::kBytes;
+    const char* kp;
+    const char* vp;
+    int64_t kts, vts;  // row strides in bytes
+    if (SRC == kSrcLists && sb.pg == kSfxPage) {
+      kts = p.sfx_k_token_stride * KV::kBytes;
+      vts = p.sfx_v_token_stride * KV::kBytes;
+      kp = reinterpret_cast<const char*>(p.sfx_k) +
+           ((int64_t)b * p.sfx_k_batch_stride + (int64_t)h * p.sfx_k_head_stride) * KV::kBytes + (int64_t)sb.ts * kts;
+      vp = reinterpret_cast<const char*>(p.sfx_v) +
+           ((int64_t)b * p.sfx_v_batch_stride + (int64_t)h * p.sfx_v_head_stride) * KV::kBytes + (int64_t)sb.ts * vts;
+    } else {
+      const int in_page = sb.ts % page_size;
+      kts = kv.k_token_stride * KV::kBytes;
+      vts = kv.v_token_stride * KV::kBytes;
+      kp = kbase + (int64_t)sb.pg * kv.k_page_stride * KV::kBytes + (int64_t)in_page * kts;
+      vp = vbase + (int64_t)sb.pg * kv.v_page_stride * KV::kBytes + (int64_t)in_page * vts;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       // rows past the unit's end re-read the subtile's first row (always valid); their weights are zero
       const int tl = (sb.ts + 4 * i + r < sb.hi) ? 4 * i + r : 0;
-      load_words<NWD>(kp + (int64_t)tl * kv.k_token_stride * KV::kBytes + lane_off, kb[i]);
-      load_words<NWD>(vp + (int64_t)tl * kv.v_token_stride * KV::kBytes + lane_off, vb[i]);
+      load_words<NWD>(kp + (int64_t)tl * kts + lane_off, kb[i]);
+      load_words<NWD>(vp + (int64_t)tl * vts + lane_off, vb[i]);
     }
   };
 
@@ -395,8 +488,10 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
     float sc = p.scale_log2;
     float vsc = 1.f;
     if constexpr (kFp8) {
-      sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
-      vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+      if (sb.pg >= 0) {
+        sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+        vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+      }
     }
     const bool valid = sb.ts + 4 * my_step + r < sb.hi;
 
@@ -560,68 +655,75 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 
 // Split-K merge of the partials of every (sequence, kv head):
 // out = sum_c acc_c 2^(m_c - M) / max(sum_c l_c 2^(m_c - M), 1e-30), M = max_c m_c
-// (the reduce of CBT/legacy.py:765-794, in the log2 domain of the partials).
-// Every one of the n_slots slots was written (empty items wrote m = -inf), so no
-// load here depends on another.
+// (the reduce of CBT/legacy.py:765-794, in the log2 domain of the partials).  The
+// slots are the finalize's n_slots items plus, in condition mode, one representative
+// partial per route chunk.  Every slot was written (empty ones with m = -inf), so
+// no load here depends on another.
+template <int D, int G>
+__device__ __forceinline__ void fold_slots(const float* ml, const float* acc, int64_t base, int n, int g, int o,
+                                           float& M, float& a, float& l) {
+  constexpr int kBatch = 8;  // slots whose loads are in flight together
+  for (int c0 = 0; c0 < n; c0 += kBatch) {
+    float mc[kBatch], lc[kBatch], ac[kBatch];
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+      const bool in = c0 + t < n;
+      const int64_t slot = base + c0 + t;
+      mc[t] = in ? ml[(slot * G + g) * 2] : kNegInf;
+      lc[t] = in ? ml[(slot * G + g) * 2 + 1] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) {
+      // an empty slot (m = -inf) never had its acc written
+      ac[t] = (mc[t] != kNegInf) ? acc[(base + c0 + t) * (G * D) + o] : 0.f;
+    }
+    float mb = kNegInf;
+#pragma unroll
+    for (int t = 0; t < kBatch; ++t) mb = fmaxf(mb, mc[t]);
+    const float m_new = fmaxf(M, mb);
+    if (m_new != kNegInf) {
+      const float fo = (M == kNegInf) ? 0.f : exp2f(M - m_new);
+      a *= fo;
+      l *= fo;
+#pragma unroll
+      for (int t = 0; t < kBatch; ++t) {
+        if (mc[t] == kNegInf) continue;
+        const float f = exp2f(mc[t] - m_new);
+        a += f * ac[t];
+        l += f * lc[t];
+      }
+    }
+    M = m_new;
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
   const int bh = blockIdx.x;
   const int b = bh / p.n_kv_heads;
   const int h = bh - b * p.n_kv_heads;
-  const int64_t pbase = (int64_t)bh * p.max_items;
-  constexpr int kBatch = 8;  // slots whose loads are in flight together
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
     const int g = o / D;
     float M = kNegInf, a = 0.f, l = 0.f;
-    for (int c0 = 0; c0 < n_slots; c0 += kBatch) {
-      float mc[kBatch], lc[kBatch], ac[kBatch];
-#pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        const bool in = c0 + t < n_slots;
-        const int64_t slot = pbase + c0 + t;
-        mc[t] = in ? p.part_ml[(slot * G + g) * 2] : kNegInf;
-        lc[t] = in ? p.part_ml[(slot * G + g) * 2 + 1] : 0.f;
-      }
-#pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        // an empty slot (m = -inf) never had its acc written
-        ac[t] = (mc[t] != kNegInf) ? p.part_acc[(pbase + c0 + t) * (G * D) + o] : 0.f;
-      }
-      float mb = kNegInf;
-#pragma unroll
-      for (int t = 0; t < kBatch; ++t) mb = fmaxf(mb, mc[t]);
-      const float m_new = fmaxf(M, mb);
-      if (m_new != kNegInf) {
-        const float fo = (M == kNegInf) ? 0.f : exp2f(M - m_new);
-        a *= fo;
-        l *= fo;
-#pragma unroll
-        for (int t = 0; t < kBatch; ++t) {
-          if (mc[t] == kNegInf) continue;
-          const float f = exp2f(mc[t] - m_new);
-          a += f * ac[t];
-          l += f * lc[t];
-        }
-      }
-      M = m_new;
-    }
+    fold_slots<D, G>(p.part_ml, p.part_acc, (int64_t)bh * p.max_items, n_slots, g, o, M, a, l);
+    if (p.rep_ml) fold_slots<D, G>(p.rep_ml, p.rep_acc, (int64_t)bh * p.n_rc, p.n_rc, g, o, M, a, l);
     store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
   }
 }
 
 // Per-instance launcher; returns IA_OK or an error code.
-template <int D, int G, typename KV, bool SPARSE>
+template <int D, int G, typename KV, int SRC>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SPARSE>), grid, dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kThreads), 0, st, p);
   int rc = check_launch("paged decode");
-  if (rc || grid.x == 1) return rc;
+  if (rc || (grid.x == 1 && !p.rep_ml)) return rc;
   hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(grid.y * grid.z), dim3(kThreads), 0, st, p,
                      (int)grid.x);
   return check_launch("split-k merge");
 }
 
 // Resident workgroups of one instance on the current device (cached).
-template <int D, int G, typename KV, bool SPARSE>
+template <int D, int G, typename KV, int SRC>
 int resident_wgs() {
   static int cached = 0;
   if (cached == 0) {
@@ -629,7 +731,7 @@ int resident_wgs() {
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SPARSE>), kThreads,
+            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC>), kThreads,
             0) != hipSuccess)
       return 0;
     cached = std::max(1, cus * per_cu);
@@ -637,9 +739,20 @@ int resident_wgs() {
   return cached;
 }
 
+// Host helpers shared by the decode entry points (paged_decode.hip).
+constexpr int kMaxItemsPerBh = 64;  // upper bound of split-K items per (sequence, kv head)
+int units_cap_items(int64_t units);
+size_t decode_ws_size(int batch, int hkv, int group, int d, int max_items);
+int check_kv(const ia_paged_kv* kv, int d);
+int check_shape(const ia_decode_shape* s);
+int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, dim3 grid, hipStream_t st,
+                    int* resident);
+int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
+                 int nsub_u, int cap_items, hipStream_t st, int* items_out);
+
 // Dispatch by kv dtype for one (D, G): defined in paged_decode_{bf16,f32,fp8}.hip.
-int dispatch_bf16(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
-int dispatch_f32(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
-int dispatch_fp8(const DecodeParams& p, int d, int g, bool sparse, dim3 grid, hipStream_t st, int* resident);
+int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
+int dispatch_f32(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
+int dispatch_fp8(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
 
 }  // namespace ia

@@ -186,6 +186,15 @@ def selection_finalize(stats, prefix, group, eps, term1_mass_exp=False):
 
     Returns ``selected [rows, nb]`` (broadcast over the group) and ``z [rows, nb]``.
     """
+    mean, z = condition_group_mean(stats, prefix, group, term1_mass_exp)
+    active = np.asarray(prefix["block_valid_counts"]).astype(np.int64) > 0
+    sel = (mean > eps) & active[None]
+    return np.repeat(sel, group, axis=0), z
+
+
+def condition_group_mean(stats, prefix, group, term1_mass_exp=False):
+    """The group-mean condition ``[Hkv, nb]`` that ``selection_finalize`` thresholds
+    (0 for empty blocks), and ``z [rows, nb]``."""
     s, delta = stats["s"], stats["delta"]
     rows, nb = s.shape
     hkv = rows // group
@@ -205,9 +214,7 @@ def selection_finalize(stats, prefix, group, eps, term1_mass_exp=False):
         term1 = 2.0 * b_all * np.exp(z - cm[:, None]) * (cosh - 1.0) / cl[:, None]
     term2 = 2.0 * b_c * np.exp(z - zm[:, None]) * tanh_half / zl[:, None]
     cond = np.where(active[None], term1 + term2, 0.0)
-    mean = cond.reshape(hkv, group, nb).sum(axis=1) / group
-    sel = (mean > eps) & active[None]
-    return np.repeat(sel, group, axis=0), z
+    return cond.reshape(hkv, group, nb).sum(axis=1) / group, z
 
 
 def condition_stats(selected, counts, prompt_len, suffix_len):

@@ -7,8 +7,8 @@
  * allocates device memory, never synchronises, and returns 0 on success or a
  * non-zero IA_ERR_* code.  ia_last_error() returns the message of the last
  * failure on the calling thread.  Scratch memory comes from a caller-owned
- * workspace whose size is given by the matching *_workspace_size() function;
- * its contents need no initialisation.  Calls that share one workspace must not
+ * workspace whose size is given by the matching *_workspace_size() function,
+ * 256-byte aligned; its contents need no initialisation.  Calls that share one workspace must not
  * overlap.  No kernel synchronises across workgroups inside a launch: multi-step
  * work (score -> select, split-K partials -> merge) is ordered by kernel
  * boundaries on the caller's stream.

@@ -71,42 +71,113 @@ __device__ __forceinline__ float round_if(float x, bool rnd) {
   return rnd ? __uint_as_float((u32)f32_to_bf16_bits(x) << 16) : x;
 }
 
-template <bool BF16>
-__device__ __forceinline__ void load_row(const void* base, int64_t off, float* out, int n) {
-  if constexpr (BF16) {
-    const unsigned short* p = reinterpret_cast<const unsigned short*>(base) + off;
-    if (n == 8) {
-      const uint4 w = *reinterpret_cast<const uint4*>(p);
-      out[0] = bf16_lo(w.x); out[1] = bf16_hi(w.x); out[2] = bf16_lo(w.y); out[3] = bf16_hi(w.y);
-      out[4] = bf16_lo(w.z); out[5] = bf16_hi(w.z); out[6] = bf16_lo(w.w); out[7] = bf16_hi(w.w);
+// Raw words of one row slice of DPL elements (bf16 pairs or floats): loads are
+// issued before any use so a wave keeps all of its rows in flight at once.
+template <bool BF16, int DPL>
+struct RawRow {
+  static constexpr int kWords = BF16 ? DPL / 2 : DPL;
+  u32 w[kWords];
+  __device__ __forceinline__ void load(const void* base, int64_t off) {
+    if constexpr (BF16) {
+      const unsigned short* p = reinterpret_cast<const unsigned short*>(base) + off;
+      if constexpr (DPL == 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(p);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
+        w[0] = v.x; w[1] = v.y;
+      }
     } else {
-      const uint2 w = *reinterpret_cast<const uint2*>(p);
-      out[0] = bf16_lo(w.x); out[1] = bf16_hi(w.x); out[2] = bf16_lo(w.y); out[3] = bf16_hi(w.y);
-    }
-  } else {
-    const float* p = reinterpret_cast<const float*>(base) + off;
-    for (int e = 0; e < n; e += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(p + e);
-      out[e] = w.x; out[e + 1] = w.y; out[e + 2] = w.z; out[e + 3] = w.w;
+      const float* p = reinterpret_cast<const float*>(base) + off;
+#pragma unroll
+      for (int e = 0; e < DPL; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p + e);
+        w[e] = __float_as_uint(v.x); w[e + 1] = __float_as_uint(v.y);
+        w[e + 2] = __float_as_uint(v.z); w[e + 3] = __float_as_uint(v.w);
+      }
     }
   }
-}
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) w[i] = 0u;
+  }
+  __device__ __forceinline__ float operator[](int e) const {
+    if constexpr (BF16) return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
+    else return __uint_as_float(w[e]);
+  }
+};
 
 __device__ __forceinline__ float q_elem(const CondParams& p, int64_t off) {
   return p.q_f32 ? reinterpret_cast<const float*>(p.q)[off]
                  : __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[off] << 16);
 }
 
-// log cosh(d) = |d| + log1p(e^{-2|d|}) - log 2, without overflow
+// log cosh(d) = |d| + log(1 + e^{-2|d|}) - log 2, without overflow
 __device__ __forceinline__ float log_cosh(float d) {
   const float a = fabsf(d);
-  return a + log1pf(__expf(-2.f * a)) - 0.69314718055994531f;
+  return a + __logf(1.f + __expf(-2.f * a)) - 0.69314718055994531f;
 }
 
-// cosh(d) - 1 = 2 sinh^2(d/2), without cancellation for small d
-__device__ __forceinline__ float cosh_m1(float d) {
-  const float sh = sinhf(0.5f * d);
-  return 2.f * sh * sh;
+// (m, l) <- log-sum-exp merge of (m, l) and (m2, l2); m = -inf marks an empty partial
+__device__ __forceinline__ void lse_merge(float& m, float& l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == kNegInf) return;
+  l = (m == kNegInf ? 0.f : l * __expf(m - mn)) + (m2 == kNegInf ? 0.f : l2 * __expf(m2 - mn));
+  m = mn;
+}
+
+// Per-row globals (z_m, z_l, c_m, c_l) of the G query rows of kv head h from the
+// 16-block chunk partials, by a whole 256-thread workgroup: every chunk's partials
+// are loaded at once (one round trip), merged per thread, then the maxima and the
+// rescaled sums are reduced over lanes and waves.  glob[v][g] in LDS on return
+// (v = 0..3 as above).
+template <int G>
+__device__ __forceinline__ void reduce_globals(const CondParams& p, int b, int h, float (*glob)[G],
+                                               float (*red)[2 * G]) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rows = p.n_kv_heads * G;
+  const int64_t plane = (int64_t)rows * p.n_chunks;
+  const float* base = p.partial + (int64_t)b * 4 * plane + (int64_t)h * G * p.n_chunks;
+  float m[2 * G], l[2 * G];  // pair i = (value v = i / G, row g = i % G)
+#pragma unroll
+  for (int i = 0; i < 2 * G; ++i) {
+    m[i] = kNegInf;
+    l[i] = 0.f;
+  }
+  for (int c = threadIdx.x; c < p.n_chunks; c += 256) {
+    float mc[2 * G], lc[2 * G];
+#pragma unroll
+    for (int i = 0; i < 2 * G; ++i) {
+      const float* row = base + (int64_t)(i % G) * p.n_chunks + c;
+      mc[i] = row[(2 * (i / G)) * plane];
+      lc[i] = row[(2 * (i / G) + 1) * plane];
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * G; ++i) lse_merge(m[i], l[i], mc[i], lc[i]);
+  }
+  float M[2 * G];
+#pragma unroll
+  for (int i = 0; i < 2 * G; ++i) {
+    const float mw = wave_max(m[i]);
+    if (lane == 0) red[wave][i] = mw;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2 * G; ++i) M[i] = fmaxf(fmaxf(red[0][i], red[1][i]), fmaxf(red[2][i], red[3][i]));
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2 * G; ++i) {
+    const float t = wave_sum(m[i] == kNegInf ? 0.f : l[i] * __expf(m[i] - M[i]));
+    if (lane == 0) red[wave][i] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * G) {
+    const int i = threadIdx.x;
+    glob[2 * (i / G)][i % G] = M[i];
+    glob[2 * (i / G) + 1][i % G] = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- selection stats
@@ -123,6 +194,27 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
   const int b = blockIdx.z;
   if (chunk >= p.n_chunks) return;  // whole wave; no workgroup barrier below
 
+  // every row of the chunk first: 4 steps x 4 rows x (k_bar, k_max, k_min)
+  const int64_t vbase = ((int64_t)b * p.n_kv_heads + h) * p.nb;
+  int cnt[4];
+  RawRow<KBH, DPL> rb[4];
+  RawRow<BDH, DPL> rh[4], rl[4];
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int j = chunk * kChunk16 + 4 * step + r;
+    const bool inb = j < p.nb;
+    cnt[step] = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
+    if (inb) {
+      const int64_t off = (vbase + j) * D + c16 * DPL;
+      rb[step].load(p.k_bar, off);
+      rh[step].load(p.k_max, off);
+      rl[step].load(p.k_min, off);
+    } else {
+      rb[step].zero();
+      rh[step].zero();
+      rl[step].zero();
+    }
+  }
   float qf[G][DPL];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -130,52 +222,48 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
     for (int e = 0; e < DPL; ++e)
       qf[g][e] = q_elem(p, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL + e);
 
-  const int64_t vbase = ((int64_t)b * p.n_kv_heads + h) * p.nb;
   float zs[4], zcs[4];
 #pragma unroll
   for (int step = 0; step < 4; ++step) {
     const int j = chunk * kChunk16 + 4 * step + r;
     const bool inb = j < p.nb;
-    const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
-    const bool active = cnt > 0;
-    float kb[DPL], kh[DPL], kl[DPL];
-    if (active) {
-      load_row<KBH>(p.k_bar, (vbase + j) * D + c16 * DPL, kb, DPL);
-      load_row<BDH>(p.k_max, (vbase + j) * D + c16 * DPL, kh, DPL);
-      load_row<BDH>(p.k_min, (vbase + j) * D + c16 * DPL, kl, DPL);
-    } else {
+    const bool active = cnt[step] > 0;
+    // upper/lower = sum q+ k_max + q- k_min / sum q+ k_min + q- k_max, i.e. with
+    // A = sum q (k_max + k_min) and B = sum |q| (k_max - k_min) >= 0:
+    // upper = (A + B)/2, lower = (A - B)/2 and delta = |A/2 - s| + B/2
+    float ksum[DPL], kdif[DPL];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) kb[e] = kh[e] = kl[e] = 0.f;
+    for (int e = 0; e < DPL; ++e) {
+      ksum[e] = rh[step][e] + rl[step][e];
+      kdif[e] = rh[step][e] - rl[step][e];
     }
-    float ps[G], pu[G], pl[G];
+    float ps[G], pa[G], pb[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float a = 0.f, u = 0.f, l = 0.f;
+      float a = 0.f, sa = 0.f, sb = 0.f;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) {
         const float qv = qf[g][e];
-        a = fmaf(qv, kb[e], a);
-        u = fmaf(qv, qv >= 0.f ? kh[e] : kl[e], u);
-        l = fmaf(qv, qv >= 0.f ? kl[e] : kh[e], l);
+        a = fmaf(qv, rb[step][e], a);
+        sa = fmaf(qv, ksum[e], sa);
+        sb = fmaf(fabsf(qv), kdif[e], sb);
       }
       ps[g] = row16_sum(a);
-      pu[g] = row16_sum(u);
-      pl[g] = row16_sum(l);
+      pa[g] = row16_sum(sa);
+      pb[g] = row16_sum(sb);
     }
     // lane c16 < G finishes row g = c16
-    float sv = 0.f, uv = 0.f, lv = 0.f;
+    float sv = 0.f, av = 0.f, bv = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g)
       if (g == c16) {
         sv = ps[g];
-        uv = pu[g];
-        lv = pl[g];
+        av = pa[g];
+        bv = pb[g];
       }
     sv *= p.scale;
-    uv *= p.scale;
-    lv *= p.scale;
-    const float dl = fmaxf(fabsf(uv - sv), fabsf(lv - sv));
-    const float z = active ? sv + __logf((float)max(cnt, 1)) : kNegInf;
+    const float dl = fabsf(0.5f * av * p.scale - sv) + 0.5f * bv * p.scale;
+    const float z = active ? sv + __logf((float)max(cnt[step], 1)) : kNegInf;
     zs[step] = z;
     zcs[step] = active ? (p.mass_exp ? z + dl : z + log_cosh(dl)) : kNegInf;
     if (c16 < G && inb) {
@@ -215,42 +303,43 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
   }
 }
 
-__global__ __launch_bounds__(256) void ia_condition_block_selection_reduce(CondParams p, int rows, int batch) {
-  const int t = blockIdx.x * 256 + threadIdx.x;
-  if (t >= rows * batch) return;
-  const int b = t / rows;
-  const int row = t - b * rows;
-  const int64_t plane = (int64_t)rows * p.n_chunks;
-  const float* base = p.partial + (int64_t)b * 4 * plane + (int64_t)row * p.n_chunks;
-#pragma unroll
-  for (int v = 0; v < 2; ++v) {
-    const float* m = base + (2 * v) * plane;
-    const float* l = base + (2 * v + 1) * plane;
-    float M = kNegInf;
-    for (int c = 0; c < p.n_chunks; ++c) M = fmaxf(M, m[c]);
-    float L = 0.f;
-    if (M != kNegInf)
-      for (int c = 0; c < p.n_chunks; ++c) L += (m[c] == kNegInf) ? 0.f : l[c] * __expf(m[c] - M);
-    p.globals[(int64_t)b * 4 * rows + (2 * v) * rows + row] = M;
-    p.globals[(int64_t)b * 4 * rows + (2 * v + 1) * rows + row] = L;
+// grid (Hkv, batch): the chunk partials of one kv head's rows -> globals [batch, 4, rows]
+template <int G>
+__global__ __launch_bounds__(256) void ia_condition_block_selection_reduce(CondParams p) {
+  __shared__ float glob[4][G];
+  __shared__ float red[4][2 * G];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  reduce_globals<G>(p, b, h, glob, red);
+  if (threadIdx.x < 4 * G) {
+    const int v = threadIdx.x / G, g = threadIdx.x % G;
+    const int rows = p.n_kv_heads * G;
+    p.globals[(int64_t)b * 4 * rows + (int64_t)v * rows + h * G + g] = glob[v][g];
   }
 }
 
-// condition of one (row, block); returns term1 + term2 (0 for an empty block)
-__device__ __forceinline__ float condition_value(float s, float dl, float z, float zm, float zl, float cm, float cl,
+// Condition of one (row, block): term1 + term2 with
+//   term1 = 2 B_all e^(z - c_m) (cosh(delta) - 1) / c_l   (mass_exp: 2 B_all e^(z + delta - c_m) / c_l)
+//   term2 = 2 b_c e^(z - z_m) tanh(delta / 2) / z_l
+// from one exponential of -delta (delta >= 0).  For delta >= 1/8
+// e^(z - c_m) (cosh(delta) - 1) = (1 - e^-delta)^2 e^(z - c_m + delta) / 2, which cannot
+// overflow before the product does; below it the Taylor series of cosh(delta) - 1 and
+// tanh(delta / 2) avoid the cancellation of 1 - e^-delta.  inv_zl = 1/z_l, inv_cl = 1/c_l.
+__device__ __forceinline__ float condition_value(float dl, float z, float zm, float inv_zl, float cm, float inv_cl,
                                                  float b_c, float b_all, bool mass_exp) {
-  float term1, tanh_half;
-  if (mass_exp) {
-    const float en = __expf(-dl);
-    tanh_half = (1.f - en) / (1.f + en);
-    term1 = 2.f * b_all * __expf(z + dl - cm) / cl;
+  const float en = __expf(-dl);
+  float tanh_half, term1;
+  if (dl < 0.125f) {
+    const float d2 = dl * dl;
+    tanh_half = 0.5f * dl * (1.f - d2 * (1.f / 12.f) + d2 * d2 * (1.f / 120.f));
+    term1 = mass_exp ? 2.f * b_all * __expf(z + dl - cm) * inv_cl
+                     : b_all * __expf(z - cm) * d2 * (1.f + d2 * (1.f / 12.f) + d2 * d2 * (1.f / 360.f)) * inv_cl;
   } else {
-    tanh_half = tanhf(0.5f * dl);
-    term1 = 2.f * b_all * __expf(z - cm) * cosh_m1(dl) / cl;
+    const float om = 1.f - en;
+    tanh_half = om / (1.f + en);
+    term1 = mass_exp ? 2.f * b_all * __expf(z + dl - cm) * inv_cl : b_all * om * om * __expf(z - cm + dl) * inv_cl;
   }
-  const float term2 = 2.f * b_c * __expf(z - zm) * tanh_half / zl;
-  (void)s;
-  return term1 + term2;
+  return term1 + 2.f * b_c * __expf(z - zm) * tanh_half * inv_zl;
 }
 
 template <int G>
@@ -275,8 +364,8 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_select(CondP
     z[g] = active ? s + lc : kNegInf;
     const float* gl = p.globals + (int64_t)b * 4 * rows;
     if (active)
-      mean += condition_value(s, dl, z[g], gl[row], gl[rows + row], gl[2 * rows + row], gl[3 * rows + row], b_c,
-                              b_all, p.mass_exp);
+      mean += condition_value(dl, z[g], gl[row], 1.f / gl[rows + row], gl[2 * rows + row], 1.f / gl[3 * rows + row],
+                              b_c, b_all, p.mass_exp);
   }
   mean /= (float)G;
   const uint8_t sel = (active && mean > p.eps) ? 1 : 0;
@@ -290,12 +379,18 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_select(CondP
 
 // ---------------------------------------------------------------- route + representatives
 
+// Selected-block list entry for the finalize: block id in the low 16 bits, its
+// valid-token count above (block ids < 65536 and counts <= 32767 are host-checked).
+__device__ __forceinline__ int32_t list_entry(int j, int cnt) { return j | (cnt << 16); }
+
 template <int D, int G, bool VBH, bool KBH, bool MASK>
 __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   constexpr int DPL = D / 16;
+  constexpr int kUnroll = 8;  // v_bar rows in flight per lane
   __shared__ float z_lds[G][kRouteChunk];
   __shared__ float red[8][G];
   __shared__ float glob[4][G];
+  __shared__ float gred[4][2 * G];
   __shared__ int wcnt[4];
   __shared__ float wacc[4][G * D];
 
@@ -310,61 +405,53 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   const int rows = p.n_kv_heads * G;
   const int j = rc * kRouteChunk + threadIdx.x;
   const bool inb = j < p.nb;
+
+  // ---- v_bar rows of the chunk (16 per 16-lane row), issued first: at low selection
+  // fractions almost every block is a representative, so they are all needed
+  constexpr int kRows = kRouteChunk / 16;
+  RawRow<VBH, DPL> vr[kRows];
+#pragma unroll
+  for (int t = 0; t < kRows; ++t) {
+    const int jj = rc * kRouteChunk + 16 * t + 4 * wave + r;
+    if (jj < p.nb) vr[t].load(p.v_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
+    else vr[t].zero();
+  }
+
+  // ---- this thread's block: count and statistics, loaded before the globals reduce
   const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
+  float s_g[G], d_g[G];
+  float b_c = 0.f, b_all = 0.f;
+  bool msel = false;
+  if constexpr (MASK) {
+    msel = inb && p.mask[(int64_t)bh * p.nb + j] != 0;
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t o = ((int64_t)b * rows + h * G + g) * p.nb + j;
+      s_g[g] = inb ? p.s[o] : 0.f;
+      d_g[g] = inb ? p.delta[o] : 0.f;
+    }
+    b_c = inb ? p.v_norm_max[(int64_t)bh * p.nb + j] : 0.f;
+    b_all = p.v_norm_all[bh];
+    reduce_globals<G>(p, b, h, glob, gred);
+  }
   const bool active = cnt > 0;
   const float logc = __logf((float)max(cnt, 1));
-
-  // ---- per-row globals from the stats partials (condition mode)
-  if constexpr (!MASK) {
-    const int64_t plane = (int64_t)rows * p.n_chunks;
-    for (int g = 0; g < G; ++g) {
-      const float* base = p.partial + (int64_t)b * 4 * plane + (int64_t)(h * G + g) * p.n_chunks;
-#pragma unroll
-      for (int v = 0; v < 2; ++v) {
-        const float* m = base + (2 * v) * plane;
-        const float* l = base + (2 * v + 1) * plane;
-        float M = kNegInf;
-        for (int c = threadIdx.x; c < p.n_chunks; c += 256) M = fmaxf(M, m[c]);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        if (lane == 0) red[wave][0] = M;
-        __syncthreads();
-        M = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-        __syncthreads();
-        float L = 0.f;
-        if (M != kNegInf)
-          for (int c = threadIdx.x; c < p.n_chunks; c += 256) L += (m[c] == kNegInf) ? 0.f : l[c] * __expf(m[c] - M);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
-        if (lane == 0) red[wave][0] = L;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-          glob[2 * v][g] = M;
-          glob[2 * v + 1][g] = red[0][0] + red[1][0] + red[2][0] + red[3][0];
-        }
-        __syncthreads();
-      }
-    }
-  }
 
   // ---- routing of this thread's block
   bool sel = false;
   if constexpr (MASK) {
-    sel = active && p.mask[((int64_t)b * p.n_kv_heads + h) * p.nb + j] != 0;
+    sel = active && msel;
 #pragma unroll
     for (int g = 0; g < G; ++g) z_lds[g][threadIdx.x] = kNegInf;  // logits computed below
   } else {
-    const float b_c = active ? p.v_norm_max[((int64_t)b * p.n_kv_heads + h) * p.nb + j] : 0.f;
-    const float b_all = p.v_norm_all[(int64_t)b * p.n_kv_heads + h];
     float z[G], mean = 0.f;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const int64_t o = ((int64_t)b * rows + h * G + g) * p.nb + j;
-      const float s = active ? p.s[o] : 0.f;
-      const float dl = active ? p.delta[o] : 0.f;
-      z[g] = active ? s + logc : kNegInf;
-      if (active) mean += condition_value(s, dl, z[g], glob[0][g], glob[1][g], glob[2][g], glob[3][g], b_c, b_all,
-                                          p.mass_exp);
+      z[g] = active ? s_g[g] + logc : kNegInf;
+      if (active)
+        mean += condition_value(d_g[g], z[g], glob[0][g], 1.f / glob[1][g], glob[2][g], 1.f / glob[3][g], b_c, b_all,
+                                p.mass_exp);
     }
     mean /= (float)G;
     sel = active && mean > p.eps;
@@ -376,13 +463,15 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
     for (int g = 0; g < G; ++g) p.selected[((int64_t)b * rows + h * G + g) * p.nb + j] = sel ? 1 : 0;
   }
 
-  // ---- compaction of the selected block ids, ascending
+  // ---- compaction of the selected blocks, ascending
   const unsigned long long ballot = __ballot(sel);
   if (lane == 0) wcnt[wave] = __popcll(ballot);
   __syncthreads();
   int off = 0;
   for (int w = 0; w < wave; ++w) off += wcnt[w];
-  if (sel) p.rc_lists[((int64_t)bh * p.n_rc + rc) * kRouteChunk + off + __popcll(ballot & ((1ull << lane) - 1ull))] = j;
+  if (sel)
+    p.rc_lists[((int64_t)bh * p.n_rc + rc) * kRouteChunk + off + __popcll(ballot & ((1ull << lane) - 1ull))] =
+        list_entry(j, cnt);
   if (threadIdx.x == 0) p.rc_counts[(int64_t)bh * p.n_rc + rc] = wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
 
   // ---- fixed-mask mode: representative logits q.k_bar/sqrt(D) + log(count)
@@ -396,28 +485,30 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
         qb[g][e] = round_if(qv, p.rep_bf16);
       }
     __syncthreads();  // z_lds initialised
-    for (int t = 0; t < kRouteChunk / 16; ++t) {
-      const int jl = 16 * t + 4 * wave + r;  // local block row
-      const int jj = rc * kRouteChunk + jl;
-      const bool in2 = jj < p.nb;
-      const int cnt2 = in2 ? p.counts[(int64_t)b * p.nb + jj] : 0;
-      const bool rep = cnt2 > 0 && p.mask[((int64_t)b * p.n_kv_heads + h) * p.nb + jj] == 0;
-      float kb[DPL];
-      if (rep) {
-        load_row<KBH>(p.k_bar, (((int64_t)b * p.n_kv_heads + h) * p.nb + jj) * D + c16 * DPL, kb, DPL);
+    for (int t0 = 0; t0 < kRouteChunk / 16; t0 += kUnroll) {
+      RawRow<KBH, DPL> kr[kUnroll];
+      int cu[kUnroll];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) kb[e] = round_if(kb[e], p.rep_bf16);
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) kb[e] = 0.f;
+      for (int u = 0; u < kUnroll; ++u) {
+        const int jj = rc * kRouteChunk + 16 * (t0 + u) + 4 * wave + r;
+        const bool in2 = jj < p.nb;
+        cu[u] = in2 ? p.counts[(int64_t)b * p.nb + jj] : 0;
+        const bool rep = cu[u] > 0 && p.mask[(int64_t)bh * p.nb + jj] == 0;
+        cu[u] = rep ? cu[u] : 0;
+        if (rep) kr[u].load(p.k_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
+        else kr[u].zero();
       }
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float a = 0.f;
+      for (int u = 0; u < kUnroll; ++u) {
+        const int jl = 16 * (t0 + u) + 4 * wave + r;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) a = fmaf(qb[g][e], kb[e], a);
-        a = row16_sum(a);
-        if (c16 == 0 && rep) z_lds[g][jl] = a * p.scale + __logf((float)cnt2);
+        for (int g = 0; g < G; ++g) {
+          float a = 0.f;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) a = fmaf(qb[g][e], round_if(kr[u][e], !KBH && p.rep_bf16), a);
+          a = row16_sum(a);
+          if (c16 == 0 && cu[u] > 0) z_lds[g][jl] = a * p.scale + __logf((float)cu[u]);
+        }
       }
     }
   }
@@ -453,25 +544,14 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
-  for (int t = 0; t < kRouteChunk / 16; ++t) {
+#pragma unroll
+  for (int t = 0; t < kRows; ++t) {
     const int jl = 16 * t + 4 * wave + r;
-    const int jj = rc * kRouteChunk + jl;
-    float bw[G];
-    bool any = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      bw[g] = z_lds[g][jl];
-      any |= bw[g] != 0.f;
-    }
-    if (!any || jj >= p.nb) continue;
-    float vb[DPL];
-    load_row<VBH>(p.v_bar, (((int64_t)b * p.n_kv_heads + h) * p.nb + jj) * D + c16 * DPL, vb, DPL);
+      const float bw = round_if(z_lds[g][jl], p.rep_bf16);
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float wq = round_if(bw[g], p.rep_bf16);
-#pragma unroll
-      for (int e = 0; e < DPL; ++e)
-        acc[g][e] = fmaf(wq, round_if(vb[e], p.rep_bf16), acc[g][e]);
+      for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(bw, round_if(vr[t][e], !VBH && p.rep_bf16), acc[g][e]);
     }
   }
 #pragma unroll
@@ -506,8 +586,8 @@ int check_summaries(const ia_block_summaries* sm, bool need_bounds, bool need_v)
   const int32_t dts[3] = {sm->k_bar_dtype, sm->bounds_dtype, sm->v_bar_dtype};
   for (int32_t dt : dts)
     if (dt != IA_F32 && dt != IA_BF16) return fail(IA_ERR_INVALID, "summary dtypes must be IA_F32 or IA_BF16");
-  if (sm->nb < 0 || sm->block_size <= 0 || sm->block_size % 16)
-    return fail(IA_ERR_INVALID, "nb must be >= 0 and block_size a positive multiple of 16");
+  if (sm->nb < 0 || sm->block_size <= 0 || sm->block_size % 16 || sm->block_size > 32768)
+    return fail(IA_ERR_INVALID, "nb must be >= 0 and block_size a positive multiple of 16, at most 32768");
   const void* ptrs[4] = {sm->k_bar, sm->k_max, sm->k_min, sm->v_bar};
   for (const void* q : ptrs)
     if (reinterpret_cast<uintptr_t>(q) % 16) return fail(IA_ERR_INVALID, "summary arrays must be 16-byte aligned");
@@ -649,6 +729,8 @@ int run_condition(bool mask_mode, const ia_decode_shape* shape, const void* q, c
   const CondWs need = cond_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb, cap_items, nullptr);
   if (!workspace || workspace_bytes < need.total)
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need.total) + " bytes");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (shape->batch == 0) return IA_OK;
   const CondWs ws = cond_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb, cap_items,
                                    reinterpret_cast<char*>(workspace));
@@ -696,7 +778,6 @@ int run_condition(bool mask_mode, const ia_decode_shape* shape, const void* q, c
   p.rc_counts = ws.rc_counts;
   p.rc_lists = ws.rc_lists;
   p.n_rc = nb > 0 ? n_rc : 0;
-  p.blk_counts = sm->counts;
   p.nb_max = nb;
   if (sfx_cap > 0) {
     p.sfx_k = sfx->k;
@@ -759,9 +840,13 @@ int ia_condition_selection_stats(const ia_decode_shape* shape, const void* q, co
   IA_DG_SWITCH(D, G, (launch_stats<DD, GG>(cp, kbh, bdh, shape->batch, st)));
   rc = check_launch("condition stats");
   if (rc || !globals) return rc;
-  const int rows = shape->n_q_heads;
-  hipLaunchKernelGGL(ia_condition_block_selection_reduce, dim3((rows * shape->batch + 255) / 256), dim3(256), 0, st,
-                     cp, rows, shape->batch);
+  const dim3 grid(shape->n_kv_heads, shape->batch);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(ia_condition_block_selection_reduce<1>, grid, dim3(256), 0, st, cp); break;
+    case 2: hipLaunchKernelGGL(ia_condition_block_selection_reduce<2>, grid, dim3(256), 0, st, cp); break;
+    case 4: hipLaunchKernelGGL(ia_condition_block_selection_reduce<4>, grid, dim3(256), 0, st, cp); break;
+    default: hipLaunchKernelGGL(ia_condition_block_selection_reduce<8>, grid, dim3(256), 0, st, cp); break;
+  }
   return check_launch("condition reduce");
 }
 

@@ -106,6 +106,26 @@ __device__ __forceinline__ void reduce_scatter16(float* v, int lane) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp<kDppRowMirror>(v));
+  v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  return v;
+}
+
+// Reductions over the 64 lanes of a wave; every lane receives the result.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += shfl_xor_f(v, 16);
+  return v + shfl_xor_f(v, 32);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, shfl_xor_f(v, 16));
+  return fmaxf(v, shfl_xor_f(v, 32));
+}
+
 // Wave-level barrier for LDS traffic that stays inside one wavefront.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

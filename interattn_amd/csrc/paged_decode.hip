@@ -115,6 +115,8 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   const size_t need = decode_ws_size(shape->batch, shape->n_kv_heads, G, D, cap_items);
   if (cap_items > 1 && (!workspace || workspace_bytes < need))
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (shape->batch == 0) return IA_OK;
 
   DecodeParams p{};

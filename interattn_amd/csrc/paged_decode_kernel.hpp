@@ -78,6 +78,8 @@ constexpr int kSrcLists = 2;  // route-chunk lists of selected blocks, then the 
 
 constexpr int kRouteChunk = 256;      // blocks per route workgroup (condition mode)
 constexpr int kMaxRouteChunks = 256;  // route chunks per (sequence, kv head)
+constexpr int kMaxItemsPerBh = 64;  // upper bound of split-K items per (sequence, kv head)
+constexpr int kSpecEntries = 2048;  // list entries a finalize item stages without waiting for the counts
 constexpr int kNoPage = -1;
 constexpr int kSfxPage = -2;          // subtile of the contiguous suffix source
 
@@ -95,7 +97,6 @@ struct DecodeParams {
   const int32_t* rc_counts;   // [batch*Hkv, n_rc]
   const int32_t* rc_lists;    // [batch*Hkv, n_rc, kRouteChunk]
   int32_t n_rc;
-  const int32_t* blk_counts;  // [batch, nb_max]
   int32_t nb_max;
   const void* sfx_k;
   const void* sfx_v;
@@ -217,8 +218,11 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
-  __shared__ int sub_page[kMaxSubsPerItem];
+  __shared__ int sub_pg[kMaxSubsPerItem];    // page id of each valid subtile (kSfxPage: suffix)
+  __shared__ int sub_info[kMaxSubsPerItem];  // first row in the page (or suffix token) << 5 | valid rows
+  __shared__ int wcnt_p[kWaves];
   __shared__ int rc_prefix[SRC == kSrcLists ? kMaxRouteChunks + 1 : 1];
+  __shared__ int rc_entries[SRC == kSrcLists ? kSpecEntries : 1];
   __shared__ float wacc_lds[kWaves][G * D];
   __shared__ float wm_lds[kWaves][G];
   __shared__ float wl_lds[kWaves][G];
@@ -232,6 +236,28 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   const int b = blockIdx.z;
   const int bh = b * p.n_kv_heads + h;
 
+  // ---- query rows of this kv head, in the lane's dim slice: raw loads issued first
+  // (independent of the prologue), converted after it
+  u32 qraw[G][DPL];  // f32 q: DPL floats; bf16 q: DPL/2 pairs
+  {
+    const int d0 = c16 * DPL;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
+      if (p.q_f32) {
+        const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) qraw[g][e] = qp[e];
+      } else {
+        const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) qraw[g][e] = (u32)qp[2 * e] | ((u32)qp[2 * e + 1] << 16);
+#pragma unroll
+        for (int e = DPL / 2; e < DPL; ++e) qraw[g][e] = 0u;
+      }
+    }
+  }
+
   const int seq_len = (SRC == kSrcLists) ? 0 : max(p.seq_lens[b], 0);
   int n_units, n_blk_units = 0, sfx_len = 0;
   if constexpr (SRC == kSrcTopk) {
@@ -239,7 +265,13 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   } else if constexpr (SRC == kSrcDense) {
     n_units = (seq_len + p.unit_tokens - 1) / p.unit_tokens;
   } else {
-    // selected blocks of every route chunk (exclusive prefix in LDS), then the suffix tiles
+    // selected blocks of every route chunk (exclusive prefix in LDS), then the suffix tiles.
+    // With few route chunks every list entry is staged in the same round trip as the
+    // counts (entries past a chunk's count are never used).
+    if (p.n_rc * kRouteChunk <= kSpecEntries) {
+      const int32_t* src = p.rc_lists + (int64_t)bh * p.n_rc * kRouteChunk;
+      for (int t = threadIdx.x; t < p.n_rc * kRouteChunk; t += kThreads) rc_entries[t] = src[t];
+    }
     if (wave == 0) {
       int run = 0;
       for (int c0 = 0; c0 < p.n_rc; c0 += 64) {
@@ -303,10 +335,14 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
           if (rc_prefix[mid] <= u) lo_c = mid;
           else hi_c = mid - 1;
         }
-        const int j = p.rc_lists[((int64_t)bh * p.n_rc + lo_c) * kRouteChunk + (u - rc_prefix[lo_c])];
-        if (j >= 0 && j < p.nb_max) {
+        // entry = block id | valid tokens << 16 (written by the route kernel)
+        const int idx = lo_c * kRouteChunk + (u - rc_prefix[lo_c]);
+        const int e = (p.n_rc * kRouteChunk <= kSpecEntries) ? rc_entries[idx]
+                                                            : p.rc_lists[(int64_t)bh * p.n_rc * kRouteChunk + idx];
+        const int j = e & 0xffff;
+        if (e >= 0 && j < p.nb_max) {
           lo = j * p.unit_tokens;
-          hi = lo + max(0, min(p.blk_counts[(int64_t)b * p.nb_max + j], p.unit_tokens));
+          hi = lo + max(0, min(e >> 16, p.unit_tokens));
         }
       } else {
         lo = (u - n_blk_units) * kDenseTile;
@@ -318,58 +354,78 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
     unit_hi[t] = sfx ? -hi - 1 : hi;  // suffix units carry a negative end
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < nu * nsub_u; t += kThreads) {
-    const int u = t / nsub_u;
-    const int lo = unit_lo[u];
-    const int hi_raw = unit_hi[u];
-    const bool sfx = hi_raw < 0;
-    const int hi = sfx ? -hi_raw - 1 : hi_raw;
-    const int tok = lo + 16 * (t - u * nsub_u);
-    int pg = kNoPage;
-    if (tok < hi) {
-      if (sfx) {
-        pg = kSfxPage;
-      } else {
-        const int lp = tok / page_size;
-        if (!bt_row) {
-          pg = lp;
-        } else if (lp < kv.bt_cols) {
-          pg = bt_row[lp];
+  // valid subtiles of the item in ascending order, compacted (ballots + per-wave counts)
+  int n_sub = 0;  // uniform
+  for (int t0 = 0; t0 < nu * nsub_u; t0 += kThreads) {
+    const int t = t0 + threadIdx.x;
+    int pg = kNoPage, info = 0;
+    if (t < nu * nsub_u) {
+      const int u = t / nsub_u;
+      const int lo = unit_lo[u];
+      const int hi_raw = unit_hi[u];
+      const bool sfx = hi_raw < 0;
+      const int hi = sfx ? -hi_raw - 1 : hi_raw;
+      const int tok = lo + 16 * (t - u * nsub_u);
+      if (tok < hi) {
+        const int nv = min(16, hi - tok);
+        if (sfx) {
+          pg = kSfxPage;
+          info = (tok << 5) | nv;
+        } else {
+          const int lp = tok / page_size;
+          if (!bt_row) {
+            pg = lp;
+          } else if (lp < kv.bt_cols) {
+            pg = bt_row[lp];
+          }
+          if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = kNoPage;
+          info = ((tok - lp * page_size) << 5) | nv;
         }
-        if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = kNoPage;
       }
     }
-    sub_page[t] = pg;
+    const bool ok = pg != kNoPage;
+    const unsigned long long bal = __ballot(ok);
+    if (lane == 0) wcnt_p[wave] = __popcll(bal);
+    __syncthreads();
+    int off = n_sub;
+    for (int w = 0; w < wave; ++w) off += wcnt_p[w];
+    if (ok) {
+      const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
+      sub_pg[k] = pg;
+      sub_info[k] = info;
+    }
+    n_sub += wcnt_p[0] + wcnt_p[1] + wcnt_p[2] + wcnt_p[3];
+    __syncthreads();
   }
 
-  // ---- query rows of this kv head, in the lane's dim slice
+  __syncthreads();
+
   constexpr int QW = kBf16 ? DPL / 2 : DPL;  // bf16 pairs or floats
   u32 qw[G][QW];
-  {
-    const int d0 = c16 * DPL;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
-      float qf[DPL];
-      if (p.q_f32) {
-        const float* qp = reinterpret_cast<const float*>(p.q) + row + d0;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) qf[e] = qp[e];
-      } else {
-        const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) qf[e] = __uint_as_float((u32)qp[e] << 16);
-      }
+  for (int g = 0; g < G; ++g) {
+    if (p.q_f32) {
       if constexpr (kBf16) {
 #pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) qw[g][e] = pack_bf16x2(qf[2 * e], qf[2 * e + 1]);
+        for (int e = 0; e < DPL / 2; ++e)
+          qw[g][e] = pack_bf16x2(__uint_as_float(qraw[g][2 * e]), __uint_as_float(qraw[g][2 * e + 1]));
       } else {
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) qw[g][e] = __float_as_uint(qf[e]);
+        for (int e = 0; e < DPL; ++e) qw[g][e] = qraw[g][e];
+      }
+    } else {
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) qw[g][e] = qraw[g][e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL / 2; ++e) {
+          qw[g][2 * e] = __float_as_uint(bf16_lo(qraw[g][e]));
+          qw[g][2 * e + 1] = __float_as_uint(bf16_hi(qraw[g][e]));
+        }
       }
     }
   }
-  __syncthreads();
 
   const char* kbase = reinterpret_cast<const char*>(kv.k) + (int64_t)h * kv.k_head_stride * KV::kBytes;
   const char* vbase = reinterpret_cast<const char*>(kv.v) + (int64_t)h * kv.v_head_stride * KV::kBytes;
@@ -400,32 +456,22 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 #pragma unroll
     for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
 
-  // ---- subtile iterator over this wave's units (u = wave, wave + 4, ...)
+  // ---- subtile iterator: wave w takes the item's valid subtiles w, w + 4, ...
   struct Sub {
-    int u;   // local unit index; >= nu when exhausted
-    int s;   // subtile within the unit
-    int ts;  // first token
-    int hi;  // end of the unit's valid tokens
-    int pg;  // page id
+    int k;    // index in the compacted list; >= n_sub when exhausted
+    int pg;   // page id (kSfxPage: suffix)
+    int row;  // first row within the page (suffix: first suffix token)
+    int nv;   // valid rows, 1..16
   };
-  auto seek = [&](int u, int s) -> Sub {
-    while (u < nu) {
-      const int lo = unit_lo[u];
-      int hi = unit_hi[u];
-      if (hi < 0) hi = -hi - 1;  // suffix unit
-      for (; lo + 16 * s < hi; ++s) {
-        const int pg = sub_page[u * nsub_u + s];
-        if (pg != kNoPage) return Sub{u, s, lo + 16 * s, hi, pg};
-      }
-      u += kWaves;
-      s = 0;
-    }
-    return Sub{nu, 0, 0, 0, -1};
+  auto seek = [&](int k) -> Sub {
+    if (k >= n_sub) return Sub{n_sub, 0, 0, 0};
+    const int info = sub_info[k];
+    return Sub{k, sub_pg[k], info >> 5, info & 31};
   };
-  auto next = [&](const Sub& c) -> Sub { return c.u < nu ? seek(c.u, c.s + 1) : c; };
+  auto next = [&](const Sub& c) -> Sub { return seek(c.k + kWaves); };
 
   auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
-    if (sb.u >= nu) return;
+    if (sb.k >= n_sub) return;
     const char* kp;
     const char* vp;
     int64_t kts, vts;  // row strides in bytes
@@ -433,20 +479,19 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
       kts = p.sfx_k_token_stride * KV::kBytes;
       vts = p.sfx_v_token_stride * KV::kBytes;
       kp = reinterpret_cast<const char*>(p.sfx_k) +
-           ((int64_t)b * p.sfx_k_batch_stride + (int64_t)h * p.sfx_k_head_stride) * KV::kBytes + (int64_t)sb.ts * kts;
+           ((int64_t)b * p.sfx_k_batch_stride + (int64_t)h * p.sfx_k_head_stride) * KV::kBytes + (int64_t)sb.row * kts;
       vp = reinterpret_cast<const char*>(p.sfx_v) +
-           ((int64_t)b * p.sfx_v_batch_stride + (int64_t)h * p.sfx_v_head_stride) * KV::kBytes + (int64_t)sb.ts * vts;
+           ((int64_t)b * p.sfx_v_batch_stride + (int64_t)h * p.sfx_v_head_stride) * KV::kBytes + (int64_t)sb.row * vts;
     } else {
-      const int in_page = sb.ts % page_size;
       kts = kv.k_token_stride * KV::kBytes;
       vts = kv.v_token_stride * KV::kBytes;
-      kp = kbase + (int64_t)sb.pg * kv.k_page_stride * KV::kBytes + (int64_t)in_page * kts;
-      vp = vbase + (int64_t)sb.pg * kv.v_page_stride * KV::kBytes + (int64_t)in_page * vts;
+      kp = kbase + (int64_t)sb.pg * kv.k_page_stride * KV::kBytes + (int64_t)sb.row * kts;
+      vp = vbase + (int64_t)sb.pg * kv.v_page_stride * KV::kBytes + (int64_t)sb.row * vts;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      // rows past the unit's end re-read the subtile's first row (always valid); their weights are zero
-      const int tl = (sb.ts + 4 * i + r < sb.hi) ? 4 * i + r : 0;
+      // rows past the subtile's valid rows re-read its first row (always valid); their weights are zero
+      const int tl = (4 * i + r < sb.nv) ? 4 * i + r : 0;
       load_words<NWD>(kp + (int64_t)tl * kts + lane_off, kb[i]);
       load_words<NWD>(vp + (int64_t)tl * vts + lane_off, vb[i]);
     }
@@ -493,7 +538,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
         vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
       }
     }
-    const bool valid = sb.ts + 4 * my_step + r < sb.hi;
+    const bool valid = 4 * my_step + r < sb.nv;
 
     // ---------------- online softmax, one update per subtile
     float pw[KG], m_new[KG];
@@ -574,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   constexpr int NBUF = KV::kRing;
   u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD];
   Sub ring[NBUF];
-  ring[0] = seek(wave, 0);
+  ring[0] = seek(wave);
   issue(ring[0], kbuf[0], vbuf[0]);
 #pragma unroll
   for (int k = 1; k < NBUF - 1; ++k) {
@@ -587,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
     for (int k = 0; k < NBUF; ++k) {
       const int fk = (k + NBUF - 1) % NBUF;  // free buffer
       const int pk = (k + NBUF - 2) % NBUF;  // most recently issued
-      if (ring[k].u >= nu) {
+      if (ring[k].k >= n_sub) {
         done = true;
         break;
       }
@@ -653,61 +698,124 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   }
 }
 
-// Split-K merge of the partials of every (sequence, kv head):
-// out = sum_c acc_c 2^(m_c - M) / max(sum_c l_c 2^(m_c - M), 1e-30), M = max_c m_c
-// (the reduce of CBT/legacy.py:765-794, in the log2 domain of the partials).  The
-// slots are the finalize's n_slots items plus, in condition mode, one representative
-// partial per route chunk.  Every slot was written (empty ones with m = -inf), so
-// no load here depends on another.
-template <int D, int G>
-__device__ __forceinline__ void fold_slots(const float* ml, const float* acc, int64_t base, int n, int g, int o,
-                                           float& M, float& a, float& l) {
-  constexpr int kBatch = 8;  // slots whose loads are in flight together
-  for (int c0 = 0; c0 < n; c0 += kBatch) {
-    float mc[kBatch], lc[kBatch], ac[kBatch];
-#pragma unroll
-    for (int t = 0; t < kBatch; ++t) {
-      const bool in = c0 + t < n;
-      const int64_t slot = base + c0 + t;
-      mc[t] = in ? ml[(slot * G + g) * 2] : kNegInf;
-      lc[t] = in ? ml[(slot * G + g) * 2 + 1] : 0.f;
-    }
-#pragma unroll
-    for (int t = 0; t < kBatch; ++t) {
-      // an empty slot (m = -inf) never had its acc written
-      ac[t] = (mc[t] != kNegInf) ? acc[(base + c0 + t) * (G * D) + o] : 0.f;
-    }
-    float mb = kNegInf;
-#pragma unroll
-    for (int t = 0; t < kBatch; ++t) mb = fmaxf(mb, mc[t]);
-    const float m_new = fmaxf(M, mb);
-    if (m_new != kNegInf) {
-      const float fo = (M == kNegInf) ? 0.f : exp2f(M - m_new);
-      a *= fo;
-      l *= fo;
-#pragma unroll
-      for (int t = 0; t < kBatch; ++t) {
-        if (mc[t] == kNegInf) continue;
-        const float f = exp2f(mc[t] - m_new);
-        a += f * ac[t];
-        l += f * lc[t];
-      }
-    }
-    M = m_new;
-  }
-}
+constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
 
+// Split-K merge, one workgroup per (sequence, kv head): out = sum_s f_s acc_s / sum_s f_s l_s
+// with f_s = 2^(m_s - M) over the finalize items' partials and the route chunks'
+// representative partials (CBT/legacy.py:765-794).  Two dependent global round
+// trips: every slot's (m, l) is staged in LDS at once, then the accumulators of
+// the non-empty slots are read with many loads in flight.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
+  __shared__ float m_lds[kMaxMergeSlots][G];
+  __shared__ float l_lds[kMaxMergeSlots][G];
+  __shared__ int list[kMaxMergeSlots];
+  __shared__ float lsum[G];
+  __shared__ int n_list;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int bh = blockIdx.x;
   const int b = bh / p.n_kv_heads;
   const int h = bh - b * p.n_kv_heads;
+  const int n_rep = p.rep_ml ? p.n_rc : 0;
+  const int n_all = min(n_slots + n_rep, kMaxMergeSlots);
+  auto ml_of = [&](int s) -> const float* {
+    return s < n_slots ? p.part_ml + ((int64_t)bh * p.max_items + s) * G * 2
+                       : p.rep_ml + ((int64_t)bh * p.n_rc + (s - n_slots)) * G * 2;
+  };
+  auto acc_of = [&](int s) -> const float* {
+    return s < n_slots ? p.part_acc + ((int64_t)bh * p.max_items + s) * (G * D)
+                       : p.rep_acc + ((int64_t)bh * p.n_rc + (s - n_slots)) * (G * D);
+  };
+  for (int t = threadIdx.x; t < n_all * G; t += kThreads) {
+    const int s = t / G, g = t - s * G;
+    const float* ml = ml_of(s) + g * 2;
+    m_lds[s][g] = ml[0];
+    l_lds[s][g] = ml[1];
+  }
+  __syncthreads();
+  // per row: M = max_s m_s, then f_s (kept in m_lds) and the denominator
+  for (int g = wave; g < G; g += kWaves) {
+    float M = kNegInf;
+    for (int s = lane; s < n_all; s += 64) M = fmaxf(M, m_lds[s][g]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float L = 0.f;
+    for (int s = lane; s < n_all; s += 64) {
+      const float m = m_lds[s][g];
+      const float f = (m == kNegInf) ? 0.f : exp2f(m - M);
+      m_lds[s][g] = f;
+      L += f * l_lds[s][g];
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+    if (lane == 0) lsum[g] = L;
+  }
+  __syncthreads();
+  if (wave == 0) {  // slots with any weight, ascending
+    int base = 0;
+    for (int s0 = 0; s0 < n_all; s0 += 64) {
+      const int s = s0 + lane;
+      bool any = false;
+      if (s < n_all) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) any |= m_lds[s][g] != 0.f;
+      }
+      const unsigned long long bal = __ballot(any);
+      if (any) list[base + __popcll(bal & ((1ull << lane) - 1ull))] = s;
+      base += __popcll(bal);
+    }
+    if (lane == 0) n_list = base;
+  }
+  __syncthreads();
+  // accumulators: wave w folds list entries w, w + 4, ...; lane owns PER consecutive
+  // outputs of the slot's [G, D] block (vector loads), kU slots in flight
+  constexpr int PER = G * D / 64;
+  constexpr int kU = 4;
+  const int nl = n_list;
+  const int o0 = lane * PER;
+  const int g0 = o0 / D;
+  float a[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) a[e] = 0.f;
+  for (int i0 = wave; i0 < nl; i0 += kWaves * kU) {
+    float v[kU][PER];
+    float f[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = i0 + u * kWaves;
+      const bool in = i < nl;
+      const int s = in ? list[i] : 0;
+      f[u] = in ? m_lds[s][g0] : 0.f;
+      const float* src = acc_of(s) + o0;
+      if (in) {
+        if constexpr (PER % 4 == 0) {
+#pragma unroll
+          for (int e = 0; e < PER; e += 4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(src + e);
+            v[u][e] = w4.x; v[u][e + 1] = w4.y; v[u][e + 2] = w4.z; v[u][e + 3] = w4.w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < PER; ++e) v[u][e] = src[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[u][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) a[e] = fmaf(f[u], v[u][e], a[e]);
+  }
+  __shared__ float wsum[kWaves][G * D];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) wsum[wave][o0 + e] = a[e];
+  __syncthreads();
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
-    const int g = o / D;
-    float M = kNegInf, a = 0.f, l = 0.f;
-    fold_slots<D, G>(p.part_ml, p.part_acc, (int64_t)bh * p.max_items, n_slots, g, o, M, a, l);
-    if (p.rep_ml) fold_slots<D, G>(p.rep_ml, p.rep_acc, (int64_t)bh * p.n_rc, p.n_rc, g, o, M, a, l);
-    store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
+    const float t = wsum[0][o] + wsum[1][o] + wsum[2][o] + wsum[3][o];
+    store_decode_out<G, D>(p, b, h, o, t / fmaxf(lsum[o / D], 1e-30f));
   }
 }
 
@@ -740,7 +848,6 @@ int resident_wgs() {
 }
 
 // Host helpers shared by the decode entry points (paged_decode.hip).
-constexpr int kMaxItemsPerBh = 64;  // upper bound of split-K items per (sequence, kv head)
 int units_cap_items(int64_t units);
 size_t decode_ws_size(int batch, int hkv, int group, int d, int max_items);
 int check_kv(const ia_paged_kv* kv, int d);

@@ -60,6 +60,10 @@ def summary_storage_dtypes(source_dtype, *, summary_dtype=torch.float32, mixed=F
     return k_bar_dtype, torch.bfloat16, bound
 
 
+# the reference's name (CBT/core.py:411), with the layout switches as keyword arguments
+_summary_storage_dtypes = summary_storage_dtypes
+
+
 def _kv_desc(k_block, v_block, block_size):
     """Describe ``[Hkv, nb, B, D]`` prompt views as a pool of ``nb`` pages of ``B`` tokens."""
     kv = N.PagedKV()
@@ -370,12 +374,19 @@ def _condition_block_decode_output(*, q_grouped, prompt_prefix, k_suffix, v_suff
 # ------------------------------------------------------------------ dense fallback
 
 def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0, **_kwargs):
-    """Dense decode with the HF attention-function signature (CBT/core.py:1158-1177):
-    ``query [B, Hq, 1, D]``, ``key/value [B, Hkv, T, D]`` -> ``([B, 1, Hq, D], None)``.
-    Single-token decode only; the mask of a causal single-token step hides nothing, so
-    it is not read (padding masks are not supported)."""
+    """Dense attention with the HF attention-function signature (CBT/core.py:1158-1177):
+    ``query [B, Hq, L, D]``, ``key/value [B, Hkv, T, D]`` -> ``([B, L, Hq, D], None)``.
+    Single-token decode (L == 1) runs the HIP dense paged decode; the keys it reads
+    are ``[0, n_b)`` with ``n_b`` the number of positions ``attention_mask`` allows
+    for the query (all T when no mask is given), so the allowed keys must be a
+    prefix (causal decode without left padding).  Multi-token calls (prompt prefill)
+    go to transformers' SDPA attention function, as in the reference."""
     if query.shape[2] != 1:
-        raise ValueError("the HIP dense path serves single-token decode (q_len=1)")
+        from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+        return sdpa_attention_forward(module, query, key, value, attention_mask,
+                                      dropout=float(dropout) if getattr(module, "training", False) else 0.0,
+                                      scaling=scaling, **_kwargs)
     _require_cuda(query, key, value)
     if key.shape != value.shape or key.dtype != value.dtype:
         raise ValueError("key and value must share shape and dtype")
@@ -383,6 +394,12 @@ def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scal
         raise ValueError("key/value rows must be contiguous")
     bsz, hq, _, d = query.shape
     hkv, t_len = int(key.shape[1]), int(key.shape[2])
+    if attention_mask is None:
+        seq = torch.full((bsz,), t_len, device=query.device, dtype=torch.int32)
+    else:
+        m = attention_mask[:, 0, -1, :t_len] if attention_mask.dim() == 4 else attention_mask[:, -1, :t_len]
+        allowed = m if m.dtype == torch.bool else m > torch.finfo(m.dtype).min / 2
+        seq = allowed.sum(-1).to(torch.int32).expand(bsz).contiguous()
     # each sequence is one page of ceil16(T) tokens: page b = batch entry b; the
     # kernel never reads a token at or past seq_len, so the padding is never touched
     kv = N.PagedKV()
@@ -401,7 +418,6 @@ def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scal
     sh.batch, sh.n_q_heads, sh.n_kv_heads, sh.head_dim = int(bsz), int(hq), hkv, int(d)
     sh.q_batch_stride, sh.q_row_stride = int(q.stride(0)), int(q.stride(1))
     sh.q_dtype = _code(q.dtype, "query")
-    seq = torch.full((bsz,), t_len, device=query.device, dtype=torch.int32)
     out = torch.empty((bsz, hq, d), device=query.device, dtype=query.dtype)
     lib = N.lib()
     items = lib.ia_dense_max_items(int(bsz), hkv, t_len)

@@ -113,6 +113,39 @@ IA_API int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* seq_le
                              int32_t* counts, void* stream);
 
 /*
+ * Incremental form of ia_build_block_summaries for sequences that grew from
+ * old_seq_lens[b] to seq_lens[b] tokens (device arrays; old <= new and
+ * new - old <= max_new_tokens): only blocks [old / block_size,
+ * ceil(new / block_size)) are recomputed (the partial block at the old end and
+ * every block the new tokens reach) and v_norm_all is raised to their norms.
+ * The result equals a full rebuild at seq_lens, bit for bit.  Outputs as for
+ * ia_build_block_summaries, holding the summaries at old_seq_lens on entry.
+ * The reference never refreshes its summaries (generated tokens stay an exact
+ * suffix, CBT/core.py:1325-1339); this is the serving pool's maintenance step.
+ */
+IA_API int ia_update_block_summaries(const ia_paged_kv* kv, const int32_t* old_seq_lens,
+                                     const int32_t* seq_lens, int32_t batch, int32_t n_kv_heads,
+                                     int32_t head_dim, int32_t block_size, int32_t nb_max,
+                                     int32_t max_new_tokens, void* k_bar, int32_t k_bar_dtype,
+                                     void* v_bar, int32_t v_bar_dtype, void* k_max, void* k_min,
+                                     int32_t bounds_dtype, float* v_norm_max, float* v_norm_all,
+                                     int32_t* counts, void* stream);
+
+/*
+ * Append one token's K/V per sequence into the paged pool: k_new/v_new
+ * [batch, Hkv, D] (pool dtype; rows contiguous, strides in elements) are written
+ * at logical position seq_lens[b] through the block table, then seq_lens[b] is
+ * incremented, all on the device (a captured decode step can replay it).  The
+ * page that holds the position must already be mapped (bt_cols and n_pages
+ * bound it; a position past them is skipped and its length left unchanged).
+ * bf16 and f32 pools only.  New entry point: the reference appends through
+ * transformers' KV cache (torch.cat / StaticCache index_copy).
+ */
+IA_API int ia_append_kv(const ia_paged_kv* kv, const void* k_new, const void* v_new, int64_t new_batch_stride,
+                        int64_t new_head_stride, int32_t* seq_lens, int32_t batch, int32_t n_kv_heads,
+                        int32_t head_dim, void* stream);
+
+/*
  * Top-k block selection.  score[b,h,j] = mean_g(q[b,h*G+g] . k_bar[b,h,j]) / sqrt(D)
  * (group-mean representative score of CBG/methods/quest.py:91-103 with the mean
  * key as representative).  Per (b, h) the result is the forced blocks (the

@@ -6,12 +6,14 @@ The compute path is the HIP library ``libinterattn_amd.so`` (C ABI in
 
 from ._native import NativeLibraryMissing, NativeError  # noqa: F401
 from .ops import (  # noqa: F401
+    append_kv,
     build_block_summaries,
     paged_decode,
     paged_kv,
     select_blocks_topk,
     sparse_paged_decode,
     sparse_topk_decode,
+    update_block_summaries,
     workspace_tensor,
 )
 

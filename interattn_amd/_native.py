@@ -113,6 +113,12 @@ SIGNATURES = {
         [ctypes.POINTER(PagedKV), _P, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I32, _P, _P,
          _P, _P],
     ),
+    "ia_update_block_summaries": (
+        ctypes.c_int,
+        [ctypes.POINTER(PagedKV), _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I32, _P,
+         _P, _P, _P],
+    ),
+    "ia_append_kv": (ctypes.c_int, [ctypes.POINTER(PagedKV), _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _P]),
     "ia_select_topk_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "ia_select_topk": (
         ctypes.c_int,

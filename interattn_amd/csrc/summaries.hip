@@ -25,6 +25,9 @@ struct SummaryParams {
   float* v_norm_max;
   float* v_norm_all;
   int32_t* counts;
+  // incremental mode: blocks [old_seq_lens[b] / block_size, ceil(seq_lens[b] / block_size))
+  // only, v_norm_all raised by atomic max (null: every block, full build)
+  const int32_t* old_seq_lens;
 };
 
 __device__ __forceinline__ void store_elem(void* base, int64_t off, int dtype, float v) {
@@ -75,12 +78,16 @@ __global__ __launch_bounds__(256) void ia_condition_block_summaries(SummaryParam
   const int wave = threadIdx.x >> 6;
   const int c16 = lane & 15;
   const int r = lane >> 4;
-  const int j = blockIdx.x * 4 + wave;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
+  const int seq_len = max(p.seq_lens[b], 0);
+  int j = blockIdx.x * 4 + wave;
+  if (p.old_seq_lens) {
+    j += max(p.old_seq_lens[b], 0) / p.block_size;
+    if ((int64_t)j * p.block_size >= seq_len) return;  // only blocks holding tokens are refreshed
+  }
   if (j >= p.nb_max) return;
   const ia_paged_kv& kv = p.kv;
-  const int seq_len = max(p.seq_lens[b], 0);
   const int t_lo = j * p.block_size;
   const int t_hi = min(t_lo + p.block_size, seq_len);
   const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
@@ -172,6 +179,11 @@ __global__ __launch_bounds__(256) void ia_condition_block_summaries(SummaryParam
   if (c16 == 0) {
     if (p.v_norm_max) p.v_norm_max[((int64_t)b * p.n_kv_heads + h) * p.nb_max + j] = vn;
     if (h == 0) p.counts[(int64_t)b * p.nb_max + j] = cnt;
+    // a refreshed block's norm only grows (tokens are appended), so the running
+    // maximum stays exact; values are >= 0 or -inf, whose int32 bit patterns
+    // order like the floats
+    if (p.old_seq_lens && p.v_norm_all)
+      atomicMax(reinterpret_cast<int*>(p.v_norm_all) + (int64_t)b * p.n_kv_heads + h, __float_as_int(vn));
   }
 }
 
@@ -198,12 +210,13 @@ void launch_summaries(const SummaryParams& p, int eb, dim3 grid, hipStream_t st)
 }  // namespace
 }  // namespace ia
 
-extern "C" int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* seq_lens, int32_t batch,
-                                        int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t nb_max,
-                                        void* k_bar, int32_t k_bar_dtype, void* v_bar, int32_t v_bar_dtype,
-                                        void* k_max, void* k_min, int32_t bounds_dtype, float* v_norm_max,
-                                        float* v_norm_all, int32_t* counts, void* stream) {
-  using namespace ia;
+namespace ia {
+namespace {
+
+int run_summaries(const ia_paged_kv* kv, const int32_t* old_seq_lens, const int32_t* seq_lens, int32_t batch,
+                  int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t nb_max, int32_t window_blocks,
+                  void* k_bar, int32_t k_bar_dtype, void* v_bar, int32_t v_bar_dtype, void* k_max, void* k_min,
+                  int32_t bounds_dtype, float* v_norm_max, float* v_norm_all, int32_t* counts, void* stream) {
   if (!kv || !kv->k || !kv->v || !seq_lens || !counts) return fail(IA_ERR_INVALID, "null pointer argument");
   if (head_dim != 64 && head_dim != 128) return fail(IA_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
   if (block_size <= 0 || block_size % 16) return fail(IA_ERR_INVALID, "block_size must be a positive multiple of 16");
@@ -218,10 +231,11 @@ extern "C" int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* se
   if ((kv->k_token_stride * eb) % 16 || (kv->v_token_stride * eb) % 16 || (kv->k_page_stride * eb) % 16 ||
       (kv->v_page_stride * eb) % 16 || (kv->k_head_stride * eb) % 16 || (kv->v_head_stride * eb) % 16)
     return fail(IA_ERR_INVALID, "kv strides must be 16-byte multiples");
-  if (batch == 0 || nb_max == 0) return IA_OK;
+  if (batch == 0 || nb_max == 0 || window_blocks == 0) return IA_OK;
   SummaryParams p{};
   p.kv = *kv;
   p.seq_lens = seq_lens;
+  p.old_seq_lens = old_seq_lens;
   p.n_kv_heads = n_kv_heads;
   p.block_size = block_size;
   p.nb_max = nb_max;
@@ -236,15 +250,45 @@ extern "C" int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* se
   p.v_norm_all = v_norm_all;
   p.counts = counts;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 grid((nb_max + 3) / 4, n_kv_heads, batch);
+  dim3 grid((window_blocks + 3) / 4, n_kv_heads, batch);
   if (head_dim == 128) launch_summaries<128>(p, eb, grid, st);
   else launch_summaries<64>(p, eb, grid, st);
   int rc = check_launch("block summaries");
   if (rc) return rc;
-  if (v_norm_all) {
+  if (v_norm_all && !old_seq_lens) {
     hipLaunchKernelGGL(ia_condition_block_vnorm_all, dim3(batch * n_kv_heads), dim3(256), 0, st, v_norm_max,
                        v_norm_all, nb_max);
     rc = check_launch("v_norm_all");
   }
   return rc;
+}
+
+}  // namespace
+}  // namespace ia
+
+extern "C" int ia_build_block_summaries(const ia_paged_kv* kv, const int32_t* seq_lens, int32_t batch,
+                                        int32_t n_kv_heads, int32_t head_dim, int32_t block_size, int32_t nb_max,
+                                        void* k_bar, int32_t k_bar_dtype, void* v_bar, int32_t v_bar_dtype,
+                                        void* k_max, void* k_min, int32_t bounds_dtype, float* v_norm_max,
+                                        float* v_norm_all, int32_t* counts, void* stream) {
+  return ia::run_summaries(kv, nullptr, seq_lens, batch, n_kv_heads, head_dim, block_size, nb_max, nb_max, k_bar,
+                           k_bar_dtype, v_bar, v_bar_dtype, k_max, k_min, bounds_dtype, v_norm_max, v_norm_all,
+                           counts, stream);
+}
+
+extern "C" int ia_update_block_summaries(const ia_paged_kv* kv, const int32_t* old_seq_lens, const int32_t* seq_lens,
+                                         int32_t batch, int32_t n_kv_heads, int32_t head_dim, int32_t block_size,
+                                         int32_t nb_max, int32_t max_new_tokens, void* k_bar, int32_t k_bar_dtype,
+                                         void* v_bar, int32_t v_bar_dtype, void* k_max, void* k_min,
+                                         int32_t bounds_dtype, float* v_norm_max, float* v_norm_all, int32_t* counts,
+                                         void* stream) {
+  using namespace ia;
+  if (!old_seq_lens) return fail(IA_ERR_INVALID, "old_seq_lens must be non-null");
+  if (max_new_tokens < 0) return fail(IA_ERR_INVALID, "max_new_tokens must be >= 0");
+  if (block_size <= 0) return fail(IA_ERR_INVALID, "block_size must be a positive multiple of 16");
+  // the partial block at the old end plus every block the new tokens can reach
+  const int64_t window = std::min<int64_t>((int64_t)nb_max, ((int64_t)max_new_tokens + block_size - 1) / block_size + 1);
+  return run_summaries(kv, old_seq_lens, seq_lens, batch, n_kv_heads, head_dim, block_size, nb_max, (int32_t)window,
+                       k_bar, k_bar_dtype, v_bar, v_bar_dtype, k_max, k_min, bounds_dtype, v_norm_max, v_norm_all,
+                       counts, stream);
 }

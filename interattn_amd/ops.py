@@ -177,6 +177,56 @@ def build_block_summaries(pool_k, pool_v, block_table, seq_lens, block_size, *, 
     return out
 
 
+def update_block_summaries(summ, pool_k, pool_v, block_table, old_seq_lens, seq_lens, block_size, *,
+                           max_new_tokens, scales=None):
+    """Refresh ``summ`` (a ``build_block_summaries`` dict, holding the summaries at
+    ``old_seq_lens``) in place for sequences grown to ``seq_lens``; only the blocks
+    the new tokens touch are recomputed (``max_new_tokens`` bounds the growth).
+    Equal to a full rebuild at ``seq_lens``."""
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    _require_cuda(old_seq_lens, seq_lens)
+    _check_i32(old_seq_lens, "old_seq_lens")
+    _check_i32(seq_lens, "seq_lens", tuple(old_seq_lens.shape))
+    b = int(seq_lens.shape[0])
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    kb = summ["k_bar"]
+    if kb.dim() != 4 or tuple(kb.shape[:2]) != (b, hkv) or kb.shape[3] != d or not kb.is_contiguous():
+        raise ValueError("summ['k_bar'] must be a contiguous [batch, Hkv, nb_max, D] tensor")
+    nb_max = int(kb.shape[2])
+    get = lambda k: summ.get(k)  # noqa: E731
+    v_bar, k_max, k_min, vnm, vna = get("v_bar"), get("k_max"), get("k_min"), get("v_norm_max"), get("v_norm_all")
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    rc = N.lib().ia_update_block_summaries(
+        kv, old_seq_lens.data_ptr(), seq_lens.data_ptr(), b, hkv, d, int(block_size), nb_max, int(max_new_tokens),
+        kb.data_ptr(), _code(kb.dtype, "k_bar"), p(v_bar), _code(v_bar.dtype if v_bar is not None else kb.dtype, "v_bar"),
+        p(k_max), p(k_min), _code(k_max.dtype if k_max is not None else kb.dtype, "bounds"), p(vnm), p(vna),
+        summ["block_valid_counts"].data_ptr(), _stream(pool_k))
+    N.check(rc)
+    del keep
+    return summ
+
+
+def append_kv(pool_k, pool_v, block_table, seq_lens, k_new, v_new):
+    """Write one token per sequence (``k_new, v_new [batch, Hkv, D]``) at position
+    ``seq_lens[b]`` of the paged pool and advance ``seq_lens`` in place, on the
+    device (capturable in a graph)."""
+    kv, keep = paged_kv(pool_k, pool_v, block_table)
+    _require_cuda(seq_lens, k_new, v_new)
+    _check_i32(seq_lens, "seq_lens")
+    b = int(seq_lens.shape[0])
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    for t in (k_new, v_new):
+        if tuple(t.shape) != (b, hkv, d) or t.stride(2) != 1 or t.dtype != pool_k.dtype:
+            raise ValueError("k_new/v_new must be [batch, Hkv, D] of the pool dtype with contiguous rows")
+    if k_new.stride()[:2] != v_new.stride()[:2]:
+        raise ValueError("k_new and v_new must share strides")
+    rc = N.lib().ia_append_kv(kv, k_new.data_ptr(), v_new.data_ptr(), int(k_new.stride(0)), int(k_new.stride(1)),
+                              seq_lens.data_ptr(), b, hkv, d, _stream(pool_k))
+    N.check(rc)
+    del keep
+    return seq_lens
+
+
 # --------------------------------------------------------------------------- top-k selection
 
 def select_blocks_topk(q, k_bar, seq_lens, k, *, block_size, forced_first=0, forced_last=0,

@@ -1,7 +1,8 @@
 """Benchmark of one decode-attention layer call of the top-k sparse path on one MI355X.
 
-A step is one layer call: block selection (scorer + top-k, one launch) followed by the
-sparse paged finalize (one launch, fused split-K merge).  The default workload is
+A step is one layer call, ``ia_sparse_topk_decode``: the block scorer (one launch),
+the paged finalize that selects the top-k blocks in its prologue and streams them
+(one launch), and the split-K merge (one launch).  The default workload is
 batch 16, 131072-token contexts, 32 query / 8 KV heads, head_dim
 128, KV block 128, top-64 blocks per KV head, bf16 K/V in a paged pool of 16-token
 pages in randomly permuted order, bf16 k_bar summaries.  Inputs are synthetic
@@ -95,13 +96,13 @@ def make_layer(w, dev, gen, lens, table, n_pages):
                 ws={}, out=torch.empty_like(q))
 
 
-def layer_call(L, w, table, kvec, k_cap):
-    idx, n_sel = ia.select_blocks_topk(L["q"], L["k_bar"], L["seq_lens"], w["k"] or 0, block_size=w["block"],
-                                       forced_first=w["ff"], forced_last=w["fl"], k_per_seq=kvec, k_cap=k_cap,
-                                       workspace=L["ws"])
-    ia.sparse_paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], idx, n_sel,
-                           block_size=w["block"], scales=L["scales"], out=L["out"], workspace=L["ws"])
-    return idx, n_sel
+def layer_call(L, w, table, kvec, k_cap, selection=False):
+    """One decode-attention layer call: ia_sparse_topk_decode (block scores, then the
+    paged finalize selecting the top-k in its prologue, then the split-K merge)."""
+    return ia.sparse_topk_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], L["k_bar"], w["k"] or 0,
+                                 block_size=w["block"], forced_first=w["ff"], forced_last=w["fl"], k_cap=k_cap,
+                                 k_per_seq=kvec, scales=L["scales"], out=L["out"], return_selection=selection,
+                                 workspace=L["ws"])
 
 
 def algorithmic_bytes(w, lens, n_sel_list):
@@ -238,7 +239,7 @@ def main():
 
     stream = torch.cuda.current_stream()
     # selection results of layer 0 (for byte accounting and the CPU baseline)
-    idx0, nsel0 = layer_call(layers[0], w, table, kvec, k_cap)
+    _, idx0, nsel0 = layer_call(layers[0], w, table, kvec, k_cap, selection=True)
     torch.cuda.synchronize()
     idx_h = idx0.cpu().numpy()
     nsel_h = nsel0.cpu().numpy()
@@ -297,10 +298,18 @@ def main():
     ms_total = start.elapsed_time(end)
     us_per_layer = ms_total * 1e3 / steps
 
-    # per-kernel averages (eager back-to-back launches on this stream)
-    idxs = [layer_call(L, w, table, kvec, k_cap) for L in layers]
-    torch.cuda.synchronize()
+    # per-call averages (eager back-to-back launches on this stream): the fused layer
+    # call, and the two-step path's selection and finalize (+ merge) on the same data
     nrep = max(8, args.steps // (2 * nl))
+
+    def run_call():
+        for L in layers:
+            layer_call(L, w, table, kvec, k_cap)
+
+    idxs = [ia.select_blocks_topk(L["q"], L["k_bar"], L["seq_lens"], w["k"] or 0, block_size=w["block"],
+                                  forced_first=w["ff"], forced_last=w["fl"], k_per_seq=kvec, k_cap=k_cap,
+                                  workspace={}) for L in layers]
+    torch.cuda.synchronize()
 
     def run_select():
         for L in layers:
@@ -313,8 +322,10 @@ def main():
             ia.sparse_paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], ix, ns,
                                    block_size=w["block"], scales=L["scales"], out=L["out"], workspace=L["ws"])
 
+    call_us = time_events(run_call, nrep, stream) * 1e3 / nl
     sel_us = time_events(run_select, nrep, stream) * 1e3 / nl
     fin_us = time_events(run_finalize, nrep, stream) * 1e3 / nl
+    call_gbps = total_bytes / (call_us * 1e-6) / 1e9
     fin_bytes = qo_b + kv_b
     fin_gbps = fin_bytes / (fin_us * 1e-6) / 1e9
 
@@ -378,15 +389,15 @@ def main():
         "achieved_GBps": round(total_bytes / (us_per_layer * 1e-6) / 1e9, 1),
         "pct_hbm_peak": round(100 * total_bytes / (us_per_layer * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes": {"total": total_bytes, "q_out": qo_b, "k_bar": summ_b, "selected_kv": kv_b},
-        "kernels_us": {"select_topk": round(sel_us, 3), "paged_finalize": round(fin_us, 3)},
+        "kernels_us": {"ia_sparse_topk_decode": round(call_us, 3), "two_step_select_topk": round(sel_us, 3),
+                       "two_step_finalize_merge": round(fin_us, 3)},
         "roofline": {"bound": "hbm",
-                     "kernel": "ia_condition_block_paged_finalize + ia_condition_block_splitk_merge "
-                               "(one ia_sparse_paged_decode call)",
-                     "achieved": round(fin_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(fin_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": "ia_sparse_topk_decode (topk_scores + paged_finalize + splitk_merge launches)",
+                     "achieved": round(call_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(call_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src},
+        "two_step_finalize_GBps": round(fin_gbps, 1),
         "copy_ceiling_GBps": round(copy_gbps, 1),
-        "finalize_frac_of_copy": round(fin_gbps / copy_gbps, 4),
         "dense_us": None if dense_us is None else round(dense_us, 2),
         "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
         "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us_per_layer, 2),

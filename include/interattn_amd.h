@@ -284,6 +284,29 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
                                 void* out, int32_t out_dtype, void* workspace,
                                 size_t workspace_bytes, void* stream);
 
+/*
+ * One top-k decode-attention layer call in two launches: block scores (as
+ * ia_select_topk computes them, bit for bit) by a many-workgroup scorer, then the
+ * paged finalize whose prologue stages each (sequence, kv head)'s score row in LDS
+ * and applies ia_select_topk's rule (forced blocks, k or k_per_seq, ties to the
+ * lower index) before streaming the chosen blocks; the split-K merge follows.
+ * Equal to ia_select_topk + ia_sparse_paged_decode.  idx/n_sel (optional,
+ * together) receive the selection.  Requires nb_max <= 4096 and k_cap <= 512
+ * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  Replaces the selection +
+ * finalize pair of one decode step, _select_prompt_blocks_triton +
+ * _condition_block_decode_output_fused_triton (CBT/core.py:701-744, :1035-1155),
+ * for the BASELINE's top-k rule.
+ */
+IA_API size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
+                                                   int32_t head_dim, int32_t nb_max, int32_t k_cap);
+IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
+                                 const int32_t* seq_lens, const void* k_bar, int32_t k_bar_dtype,
+                                 int64_t kbar_batch_stride, int64_t kbar_head_stride, int32_t block_size,
+                                 int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
+                                 int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale, void* out,
+                                 int32_t out_dtype, int32_t* idx, int32_t* n_sel, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* Number of split-K items per (b, h) the two decode entry points use for the
  * given workload; size the decode workspace with it.  max_seq_len must bound
  * every seq_lens[b] passed to ia_paged_decode (tokens past it are not read). */

@@ -119,6 +119,12 @@ SIGNATURES = {
          _P, _P, _P],
     ),
     "ia_append_kv": (ctypes.c_int, [ctypes.POINTER(PagedKV), _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _P]),
+    "ia_sparse_topk_decode_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "ia_sparse_topk_decode": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _P,
+         _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P, _SZ, _P],
+    ),
     "ia_select_topk_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "ia_select_topk": (
         ctypes.c_int,

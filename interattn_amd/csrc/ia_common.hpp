@@ -47,6 +47,13 @@ __device__ __forceinline__ void fp8x4_to_f32(u32 w, float* out) {
   out[3] = b[1];
 }
 
+// Two OCP e4m3fn codes (byte pair HI of w) widened to a bf16 pair: exact, since
+// every e4m3 value is a bf16 value (scale 1.0).
+template <bool HI>
+__device__ __forceinline__ u32 fp8x2_to_bf16x2(u32 w) {
+  return __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+}
+
 // ------------------------------------------------------------------ DPP within 16-lane rows
 
 constexpr int kDppRowMirror = 0x140;

@@ -154,10 +154,110 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   return dispatch_decode(p, kv->dtype, D, G, src, grid, st, nullptr);
 }
 
+// Fused top-k decode workspace: the score rows, then the split-K partials.
+size_t fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, size_t* decode_off) {
+  const size_t scores = align_up((size_t)batch * hkv * std::max(nb_max, 1) * 4, 256);
+  *decode_off = scores;
+  return scores + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap));
+}
+
+int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
+                    const void* k_bar, int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
+                    int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
+                    int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale, void* out,
+                    int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  rc = check_kv(kv, shape->head_dim);
+  if (rc) return rc;
+  if (!q || !out || !seq_lens || !k_bar) return fail(IA_ERR_INVALID, "q, out, seq_lens and k_bar must be non-null");
+  if ((idx_out == nullptr) != (n_sel_out == nullptr)) return fail(IA_ERR_INVALID, "idx and n_sel go together");
+  if (out_dtype != IA_F32 && out_dtype != IA_BF16) return fail(IA_ERR_INVALID, "out dtype must be IA_F32 or IA_BF16");
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(IA_ERR_INVALID, "scale must be positive and finite");
+  if (k_bar_dtype != IA_F32 && k_bar_dtype != IA_BF16) return fail(IA_ERR_INVALID, "k_bar dtype must be IA_F32 or IA_BF16");
+  const int eb = k_bar_dtype == IA_BF16 ? 2 : 4;
+  if ((kbar_batch_stride * eb) % 16 || (kbar_head_stride * eb) % 16 || reinterpret_cast<uintptr_t>(k_bar) % 16)
+    return fail(IA_ERR_INVALID, "k_bar rows must be 16-byte aligned");
+  if (block_size <= 0 || block_size % 16 != 0) return fail(IA_ERR_INVALID, "block_size must be a positive multiple of 16");
+  if (nb_max < 0 || k < 0 || forced_first < 0 || forced_last < 0 || k_cap <= 0)
+    return fail(IA_ERR_INVALID, "nb_max, k, forced_* must be >= 0 and k_cap > 0");
+  if (nb_max > kFusedMaxBlocks || k_cap > kMaxUnitsPerItem)
+    return fail(IA_ERR_UNSUPPORTED, "fused top-k decode takes nb_max <= " + std::to_string(kFusedMaxBlocks) +
+                                        " and k_cap <= " + std::to_string(kMaxUnitsPerItem) +
+                                        "; use ia_select_topk + ia_sparse_paged_decode");
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  size_t decode_off = 0;
+  const size_t need = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, &decode_off);
+  if (!workspace || workspace_bytes < need)
+    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (shape->batch == 0) return IA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = reinterpret_cast<char*>(workspace);
+  float* scores = reinterpret_cast<float*>(ws);
+  if (nb_max > 0) {
+    rc = run_topk_scores(shape, q, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride, seq_lens, block_size,
+                         nb_max, scores, st);
+    if (rc) return rc;
+  }
+
+  DecodeParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.kv = *kv;
+  p.seq_lens = seq_lens;
+  p.k_cap = k_cap;
+  p.unit_tokens = block_size;
+  p.nb_max = nb_max;
+  p.scores = scores;
+  p.k_per_seq = k_per_seq;
+  p.topk_k = k;
+  p.forced_first = forced_first;
+  p.forced_last = forced_last;
+  p.forced_in_k = forced_in_k;
+  p.idx_out = idx_out;
+  p.n_sel_out = n_sel_out;
+  p.n_kv_heads = shape->n_kv_heads;
+  p.scale_log2 = scale * kLog2e;
+  p.q_f32 = shape->q_dtype == IA_F32;
+  p.out_f32 = out_dtype == IA_F32;
+  p.out = out;
+  const int cap_items = units_cap_items(k_cap);
+  const int64_t bh = (int64_t)shape->batch * shape->n_kv_heads;
+  int items = 1;
+  rc = decode_items(p, kv->dtype, D, G, kSrcTopkFused, bh, k_cap, block_size / 16, cap_items, st, &items);
+  if (rc) return rc;
+  p.max_items = cap_items;
+  p.part_ml = reinterpret_cast<float*>(ws + decode_off);
+  p.part_acc = reinterpret_cast<float*>(ws + decode_off + align_up((size_t)bh * cap_items * G * 2 * 4, 256));
+  return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(items, shape->n_kv_heads, shape->batch), st,
+                         nullptr);
+}
+
 }  // namespace
 }  // namespace ia
 
 extern "C" {
+
+size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
+                                            int32_t nb_max, int32_t k_cap) {
+  size_t decode_off = 0;
+  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1), &decode_off);
+}
+
+int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
+                          const void* k_bar, int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
+                          int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq,
+                          int32_t forced_first, int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale,
+                          void* out, int32_t out_dtype, int32_t* idx, int32_t* n_sel, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+  return ia::run_topk_decode(shape, q, kv, seq_lens, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride,
+                             block_size, nb_max, k, k_per_seq, forced_first, forced_last, forced_in_k, k_cap, scale,
+                             out, out_dtype, idx, n_sel, workspace, workspace_bytes, stream);
+}
 
 size_t ia_paged_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
                                       int32_t max_items) {

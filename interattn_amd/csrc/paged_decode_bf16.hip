@@ -17,6 +17,9 @@ int run_bf16(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* res
     case kSrcLists:
       if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcLists>(), IA_OK;
       return launch_paged_finalize<D, G, KvBf16, kSrcLists>(p, grid, st);
+    case kSrcTopkFused:
+      if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcTopkFused>(), IA_OK;
+      return launch_paged_finalize<D, G, KvBf16, kSrcTopkFused>(p, grid, st);
   }
   return fail(IA_ERR_UNSUPPORTED, "unit source");
 }

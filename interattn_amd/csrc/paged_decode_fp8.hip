@@ -17,6 +17,9 @@ int run_fp8(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* resi
     case kSrcLists:
       if (resident) return *resident = resident_wgs<D, G, KvFp8, kSrcLists>(), IA_OK;
       return launch_paged_finalize<D, G, KvFp8, kSrcLists>(p, grid, st);
+    case kSrcTopkFused:
+      if (resident) return *resident = resident_wgs<D, G, KvFp8, kSrcTopkFused>(), IA_OK;
+      return launch_paged_finalize<D, G, KvFp8, kSrcTopkFused>(p, grid, st);
   }
   return fail(IA_ERR_UNSUPPORTED, "unit source");
 }

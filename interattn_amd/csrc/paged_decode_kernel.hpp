@@ -34,7 +34,7 @@
 //   weight.
 #pragma once
 
-#include "ia_common.hpp"
+#include "topk_select.hpp"
 
 namespace ia {
 
@@ -50,7 +50,7 @@ struct KvF32 {
 };
 struct KvFp8 {
   static constexpr int kBytes = 1;
-  static constexpr int kRing = 4;
+  static constexpr int kRing = 3;
 };
 
 template <int NWD>
@@ -75,6 +75,8 @@ __device__ __forceinline__ void load_words(const char* p, u32* w) {
 constexpr int kSrcTopk = 0;   // idx[b, h, 0:n_sel[b, h]] blocks of unit_tokens tokens
 constexpr int kSrcDense = 1;  // every 128-token tile of [0, seq_len)
 constexpr int kSrcLists = 2;  // route-chunk lists of selected blocks, then the exact suffix
+constexpr int kSrcTopkFused = 3;  // top-k of a score row selected in the prologue, then as kSrcTopk
+constexpr int kFusedMaxBlocks = 4096;  // score row staged in LDS by the fused top-k source
 
 constexpr int kRouteChunk = 256;      // blocks per route workgroup (condition mode)
 constexpr int kMaxRouteChunks = 256;  // route chunks per (sequence, kv head)
@@ -91,6 +93,13 @@ struct DecodeParams {
   const int32_t* idx;  // kSrcTopk
   const int32_t* n_sel;
   int32_t k_cap;
+  // kSrcTopkFused: block scores [batch*Hkv, nb_max] and the selection rule; item 0
+  // of each (b, h) also writes the chosen ids / counts when idx_out is set
+  const float* scores;
+  const int32_t* k_per_seq;
+  int32_t topk_k, forced_first, forced_last, forced_in_k;
+  int32_t* idx_out;
+  int32_t* n_sel_out;
   int32_t unit_tokens;  // tokens per unit: block_size (blocks) or the dense tile
   int32_t max_items;    // stride of the item partials per (b, h)
   // kSrcLists: selected blocks per route chunk, valid tokens per block, suffix
@@ -215,6 +224,10 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   constexpr int KG = SM::KG;
   constexpr bool kBf16 = KV::kBytes == 2;
   constexpr bool kFp8 = KV::kBytes == 1;
+  // bf16 caches, and fp8 caches whose e4m3 codes widen exactly to bf16, run Q.K and
+  // P.V as bf16 pairs through v_dot2_f32_bf16; fp32 caches stay fp32
+  constexpr bool kDot2 = kBf16 || kFp8;
+  constexpr int NWB = DPL / 2;  // bf16 words per lane per token row
 
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
@@ -223,6 +236,9 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   __shared__ int wcnt_p[kWaves];
   __shared__ int rc_prefix[SRC == kSrcLists ? kMaxRouteChunks + 1 : 1];
   __shared__ int rc_entries[SRC == kSrcLists ? kSpecEntries : 1];
+  __shared__ float fsc[SRC == kSrcTopkFused ? kFusedMaxBlocks : 1];
+  __shared__ int fsel[SRC == kSrcTopkFused ? kMaxUnitsPerItem : 1];
+  __shared__ TopkLds<kThreads> ftk;
   __shared__ float wacc_lds[kWaves][G * D];
   __shared__ float wm_lds[kWaves][G];
   __shared__ float wl_lds[kWaves][G];
@@ -262,6 +278,21 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   int n_units, n_blk_units = 0, sfx_len = 0;
   if constexpr (SRC == kSrcTopk) {
     n_units = min(max(p.n_sel[bh], 0), p.k_cap);
+  } else if constexpr (SRC == kSrcTopkFused) {
+    // the whole score row in LDS, then the shared top-k rule (every item of the row
+    // selects the same blocks; item 0 publishes them)
+    const int nbs = min((seq_len + p.unit_tokens - 1) / p.unit_tokens, p.nb_max);
+    const float* sc_row = p.scores + (int64_t)bh * p.nb_max;
+    for (int t = threadIdx.x; t < nbs; t += kThreads) fsc[t] = sc_row[t];
+    __syncthreads();
+    const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
+    const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
+    n_units = topk_select<kThreads>(
+        ftk, [&](int j) -> u32 { return order_key(fsc[j]); }, nbs, rule, [&](int pos, int j) { fsel[pos] = j; });
+    if (item == 0 && p.idx_out) {
+      for (int t = threadIdx.x; t < n_units; t += kThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
+      if (threadIdx.x == 0) p.n_sel_out[bh] = n_units;
+    }
   } else if constexpr (SRC == kSrcDense) {
     n_units = (seq_len + p.unit_tokens - 1) / p.unit_tokens;
   } else {
@@ -318,8 +349,8 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   for (int t = threadIdx.x; t < nu; t += kThreads) {
     const int u = u_begin + t;
     int lo = 0, hi = 0, sfx = 0;
-    if constexpr (SRC == kSrcTopk) {
-      const int j = p.idx[(int64_t)bh * p.k_cap + u];
+    if constexpr (SRC == kSrcTopk || SRC == kSrcTopkFused) {
+      const int j = (SRC == kSrcTopkFused) ? fsel[u] : p.idx[(int64_t)bh * p.k_cap + u];
       if (j >= 0 && (int64_t)j * p.unit_tokens < seq_len) {
         lo = j * p.unit_tokens;
         hi = min(lo + p.unit_tokens, seq_len);
@@ -400,12 +431,12 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 
   __syncthreads();
 
-  constexpr int QW = kBf16 ? DPL / 2 : DPL;  // bf16 pairs or floats
+  constexpr int QW = kDot2 ? DPL / 2 : DPL;  // bf16 pairs or floats
   u32 qw[G][QW];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (p.q_f32) {
-      if constexpr (kBf16) {
+      if constexpr (kDot2) {
 #pragma unroll
         for (int e = 0; e < DPL / 2; ++e)
           qw[g][e] = pack_bf16x2(__uint_as_float(qraw[g][2 * e]), __uint_as_float(qraw[g][2 * e + 1]));
@@ -414,7 +445,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
         for (int e = 0; e < DPL; ++e) qw[g][e] = qraw[g][e];
       }
     } else {
-      if constexpr (kBf16) {
+      if constexpr (kDot2) {
 #pragma unroll
         for (int e = 0; e < DPL / 2; ++e) qw[g][e] = qraw[g][e];
       } else {
@@ -498,33 +529,45 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   };
 
   auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+    // fp8 rows widened to bf16 pairs (exact: every e4m3 value is a bf16 value)
+    u32 kx[4][NWB], vx[4][NWB];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (kFp8) {
+#pragma unroll
+        for (int w = 0; w < NWD; ++w) {
+          kx[i][2 * w] = fp8x2_to_bf16x2<false>(kb[i][w]);
+          kx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(kb[i][w]);
+          vx[i][2 * w] = fp8x2_to_bf16x2<false>(vb[i][w]);
+          vx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(vb[i][w]);
+        }
+      } else if constexpr (kBf16) {
+#pragma unroll
+        for (int w = 0; w < NWB; ++w) {
+          kx[i][w] = kb[i][w];
+          vx[i][w] = vb[i][w];
+        }
+      }
+    }
     // ---------------- scores of the 16 tokens x G rows
     float part[NV];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (kBf16) {
+      if constexpr (kDot2) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           float a = 0.f;
 #pragma unroll
-          for (int w = 0; w < NWD; ++w)
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kb[i][w]), a, false);
+          for (int w = 0; w < NWB; ++w)
+            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kx[i][w]), a, false);
           part[i * G + g] = a;
         }
       } else {
-        float kf[DPL];
-        if constexpr (kFp8) {
-#pragma unroll
-          for (int w = 0; w < NWD; ++w) fp8x4_to_f32(kb[i][w], kf + 4 * w);
-        } else {
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) kf[e] = __uint_as_float(kb[i][e]);
-        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           float a = 0.f;
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), kf[e], a);
+          for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), __uint_as_float(kb[i][e]), a);
           part[i * G + g] = a;
         }
       }
@@ -574,17 +617,20 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
     // ---------------- weighted values: weight of (token 4i + r, g) by row broadcast
     float pb[4][G];
     WeightBcast<G, 4 * G>::run(pw, pb);
-    if constexpr (kBf16) {
+    if constexpr (kDot2) {
+      // bf16 weights (the reference's cast point); an fp8 page's V scale is folded
+      // into the weight before the rounding
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) {
         const int i1 = 2 * pr, i2 = 2 * pr + 1;
         u32 pp[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) pp[g] = pack_bf16x2(pb[i1][g], pb[i2][g]);
+        for (int g = 0; g < G; ++g) pp[g] = kFp8 ? pack_bf16x2(pb[i1][g] * vsc, pb[i2][g] * vsc)
+                                                 : pack_bf16x2(pb[i1][g], pb[i2][g]);
 #pragma unroll
-        for (int w = 0; w < NWD; ++w) {
-          const u32 lo = __builtin_amdgcn_perm(vb[i2][w], vb[i1][w], 0x05040100u);
-          const u32 hi = __builtin_amdgcn_perm(vb[i2][w], vb[i1][w], 0x07060302u);
+        for (int w = 0; w < NWB; ++w) {
+          const u32 lo = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x05040100u);
+          const u32 hi = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x07060302u);
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             acc[g][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(lo), acc[g][2 * w], false);
@@ -595,22 +641,11 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float vf[DPL];
-        if constexpr (kFp8) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int w = 0; w < NWD; ++w) fp8x4_to_f32(vb[i][w], vf + 4 * w);
-        } else {
+        for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) vf[e] = __uint_as_float(vb[i][e]);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float wgt = pb[i][g] * vsc;
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(wgt, vf[e], acc[g][e]);
-        }
-      }
+          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pb[i][g], __uint_as_float(vb[i][e]), acc[g][e]);
     }
   };
 
@@ -856,6 +891,11 @@ int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, 
                     int* resident);
 int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
                  int nsub_u, int cap_items, hipStream_t st, int* items_out);
+
+// Block scores of the fused top-k decode (select_topk.hip).
+int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
+                    int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
+                    int32_t nb_max, float* scores, hipStream_t st);
 
 // Dispatch by kv dtype for one (D, G): defined in paged_decode_{bf16,f32,fp8}.hip.
 int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);

@@ -18,7 +18,7 @@
 //       block ids in ascending order.
 //   The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
 //   with the mean key (k_bar) as the block representative.
-#include "ia_common.hpp"
+#include "topk_select.hpp"
 
 namespace ia {
 
@@ -45,18 +45,11 @@ struct SelectParams {
   int32_t lds_scores;  // score rows of up to this many blocks stay in LDS
 };
 
-__device__ __forceinline__ u32 order_key(float s) {
-  const u32 u = __float_as_uint(s);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 template <int D, int G, bool QF32, bool KBF16>
 __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(SelectParams p) {
   constexpr int DPL = D / 16;
-  __shared__ u32 hist[256];
   extern __shared__ float sc_lds[];  // p.lds_scores floats
-  __shared__ int sh_int[8];
-  __shared__ int wave_cnt[2][kSelWaves];
+  __shared__ TopkLds<kSelThreads> sel_lds;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -125,18 +118,7 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
     }
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
-      float a = 0.f;
-      if constexpr (KBF16) {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) {
-          a = fmaf(qm[2 * e], bf16_lo(w[t][e]), a);
-          a = fmaf(qm[2 * e + 1], bf16_hi(w[t][e]), a);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], __uint_as_float(w[t][e]), a);
-      }
-      a = row16_sum(a) * p.score_scale;
+      const float a = block_score<DPL, KBF16>(w[t], qm, p.score_scale);
       const int j = base + kRowsPerStep * t + 4 * wave + r;
       if (c16 == 0 && j < nb) {
         if (in_lds) sc_lds[j] = a;
@@ -151,123 +133,92 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
   __syncthreads();
   auto key_at = [&](int j) -> u32 { return order_key(in_lds ? sc_lds[j] : sc_row[j]); };
 
-  // ---- selection rule
-  const int ff = min(max(p.forced_first, 0), nb);
-  const int fl_start = max(nb - max(p.forced_last, 0), 0);
-  auto is_forced = [&](int j) { return j < ff || j >= fl_start; };
-  const int n_forced = ff + (nb - max(fl_start, ff));  // |[0,ff) U [fl_start,nb)|
-  const int n_cand = nb - n_forced;
+  // ---- selection (forced blocks, radix-select threshold, ordered compaction)
   const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.k;
-  int k_eff = p.forced_in_k ? k_b - n_forced : k_b;
-  k_eff = max(k_eff, 0);
-  const int k_room = max(p.k_cap - n_forced, 0);
-  k_eff = min(k_eff, k_room);
-
-  u32 thr = 0u;       // threshold prefix; candidates with (key & thr_mask) > thr are taken
-  u32 thr_mask = 0u;
-  int take_ties = 0;  // candidates with (key & thr_mask) == thr taken, lowest indices first
-  const bool take_all = k_eff >= n_cand;
-  if (!take_all && k_eff > 0) {
-    u32 prefix = 0u, mask = 0u;
-    int remaining = k_eff;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      if (threadIdx.x < 256) hist[threadIdx.x] = 0u;
-      __syncthreads();
-      for (int j = threadIdx.x; j < nb; j += kSelThreads) {
-        if (is_forced(j)) continue;
-        const u32 key = key_at(j);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (wave == 0) {
-        // bins in descending order: lane l owns bins 255-4l .. 252-4l
-        u32 c[4];
-        u32 tot = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          c[t] = hist[255 - 4 * lane - t];
-          tot += c[t];
-        }
-        u32 inc = tot;  // inclusive scan over lanes (descending-bin order)
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const u32 o = __shfl_up(inc, off, 64);
-          if (lane >= off) inc += o;
-        }
-        const u32 exc = inc - tot;
-        // the bin where the running count first reaches `remaining`
-        if (exc < (u32)remaining && inc >= (u32)remaining) {
-          u32 run = exc;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            if (run + c[t] >= (u32)remaining) {
-              sh_int[1] = 255 - 4 * lane - t;    // digit
-              sh_int[2] = remaining - (int)run;  // still needed inside this bin
-              sh_int[3] = (int)c[t];             // candidates inside this bin
-              break;
-            }
-            run += c[t];
-          }
-        }
-      }
-      __syncthreads();
-      const u32 digit = (u32)sh_int[1];
-      remaining = sh_int[2];
-      const int in_bin = sh_int[3];
-      prefix |= digit << shift;
-      mask |= 255u << shift;
-      __syncthreads();
-      if (remaining == in_bin) break;  // the whole bin is taken: the threshold is exact
-    }
-    thr = prefix;
-    thr_mask = mask;
-    take_ties = remaining;
-  }
-
-  // ---- ordered compaction
+  const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
   int32_t* out_idx = p.idx + (int64_t)bh * p.k_cap;
-  int base_sel = 0, base_tie = 0;
-  for (int j0c = 0; j0c < nb; j0c += kSelThreads) {
-    const int j = j0c + threadIdx.x;
-    bool forced = false, above = false, tie = false;
+  const int n = topk_select<kSelThreads>(sel_lds, key_at, nb, rule, [&](int pos, int j) { out_idx[pos] = j; });
+  if (threadIdx.x == 0) p.n_sel[bh] = n;
+}
+
+// Scores of every block for the fused top-k decode (the selection itself runs in
+// the finalize's prologue): grid (ceil(nb_max / kScoreBlocksPerWg), Hkv, batch),
+// 256 threads; wave w scores blocks kScoreBlocksPerWg*blockIdx.x + 4*(kScoreRows*w + t) + r,
+// t < kScoreRows, every row of a lane in flight at once.  Same arithmetic as the
+// selector's scoring (bit-identical scores); -inf past the sequence's end.
+constexpr int kScoreRows = 4;                         // k_bar rows per lane
+constexpr int kScoreBlocksPerWg = 4 * 4 * kScoreRows;  // 4 waves x 4 rows per load x kScoreRows
+template <int D, int G, bool QF32, bool KBF16>
+__global__ __launch_bounds__(256) void ia_condition_block_topk_scores(SelectParams p) {
+  constexpr int DPL = D / 16;
+  constexpr int EB = KBF16 ? 2 : 4;
+  constexpr int NWR = DPL * EB / 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int bh = b * p.n_kv_heads + h;
+  const int j0 = kScoreBlocksPerWg * blockIdx.x + 4 * kScoreRows * wave;
+  if (j0 >= p.nb_max) return;  // whole wave
+  const int seq_len = max(p.seq_lens[b], 0);
+  const int nb = min((seq_len + p.block_size - 1) / p.block_size, p.nb_max);
+  const char* kb = reinterpret_cast<const char*>(p.k_bar) +
+                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * EB;
+  u32 w[kScoreRows][NWR];
+#pragma unroll
+  for (int t = 0; t < kScoreRows; ++t) {
+    const int j = j0 + 4 * t + r;
     if (j < nb) {
-      forced = is_forced(j);
-      if (!forced) {
-        if (take_all) {
-          above = true;
-        } else if (k_eff > 0) {
-          const u32 key = key_at(j) & thr_mask;
-          above = key > thr;
-          tie = key == thr;
+      const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * EB;
+      if constexpr (NWR >= 4) {
+#pragma unroll
+        for (int v4 = 0; v4 < NWR; v4 += 4) {
+          const uint4 x = reinterpret_cast<const uint4*>(rowp)[v4 / 4];
+          w[t][v4] = x.x; w[t][v4 + 1] = x.y; w[t][v4 + 2] = x.z; w[t][v4 + 3] = x.w;
         }
+      } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(rowp);
+        w[t][0] = x.x; w[t][1] = x.y;
       }
+    } else {
+#pragma unroll
+      for (int e = 0; e < NWR; ++e) w[t][e] = 0u;
     }
-    // tie rank in index order
-    const unsigned long long tb = __ballot(tie);
-    const int tie_rank_in_wave = __popcll(tb & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[1][wave] = __popcll(tb);
-    __syncthreads();
-    int tie_off = base_tie;
-    for (int w = 0; w < wave; ++w) tie_off += wave_cnt[1][w];
-    const bool take_tie = tie && (tie_off + tie_rank_in_wave < take_ties);
-    const bool sel = forced || above || take_tie;
-    const unsigned long long sb = __ballot(sel);
-    const int sel_rank = __popcll(sb & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[0][wave] = __popcll(sb);
-    __syncthreads();
-    int sel_off = base_sel;
-    for (int w = 0; w < wave; ++w) sel_off += wave_cnt[0][w];
-    if (sel && sel_off + sel_rank < p.k_cap) out_idx[sel_off + sel_rank] = j;
-    int tot_s = 0, tot_t = 0;
-    for (int w = 0; w < kSelWaves; ++w) {
-      tot_s += wave_cnt[0][w];
-      tot_t += wave_cnt[1][w];
-    }
-    base_sel += tot_s;
-    base_tie += tot_t;
-    __syncthreads();
   }
-  if (threadIdx.x == 0) p.n_sel[bh] = min(base_sel, p.k_cap);
+  float qm[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) qm[e] = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      float qv;
+      if constexpr (QF32) qv = reinterpret_cast<const float*>(p.q)[row + e];
+      else qv = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
+      qm[e] += qv;  // same order as the selector's sum
+    }
+  }
+  float* sc_row = p.scores + (int64_t)bh * p.nb_max;
+#pragma unroll
+  for (int t = 0; t < kScoreRows; ++t) {
+    const float a = block_score<DPL, KBF16>(w[t], qm, p.score_scale);
+    const int j = j0 + 4 * t + r;
+    if (c16 == 0 && j < p.nb_max) sc_row[j] = j < nb ? a : kNegInf;
+  }
+}
+
+template <int D, int G>
+void launch_scores(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipStream_t st) {
+  if (qf32) {
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, true, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, true, false>), grid, dim3(256), 0, st, p);
+  } else {
+    if (kbf16) hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, false, true>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, false, false>), grid, dim3(256), 0, st, p);
+  }
 }
 
 size_t select_ws_size(int batch, int hkv, int nb_max) {
@@ -289,6 +240,36 @@ int launch_select(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipSt
 }
 
 }  // namespace
+
+int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
+                    int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
+                    int32_t nb_max, float* scores, hipStream_t st) {
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  SelectParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.k_bar = k_bar;
+  p.kb_batch_stride = kbar_batch_stride;
+  p.kb_head_stride = kbar_head_stride;
+  p.seq_lens = seq_lens;
+  p.block_size = block_size;
+  p.nb_max = nb_max;
+  p.scores = scores;
+  p.n_kv_heads = shape->n_kv_heads;
+  p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
+  const dim3 grid((nb_max + kScoreBlocksPerWg - 1) / kScoreBlocksPerWg, shape->n_kv_heads, shape->batch);
+  const bool qf32 = shape->q_dtype == IA_F32;
+  const bool kbf16 = k_bar_dtype == IA_BF16;
+#define IA_SC(DD, GG) \
+  if (D == DD && G == GG) { launch_scores<DD, GG>(p, qf32, kbf16, grid, st); return check_launch("topk scores"); }
+  IA_SC(128, 4) IA_SC(128, 8) IA_SC(128, 2) IA_SC(128, 1)
+  IA_SC(64, 4) IA_SC(64, 8) IA_SC(64, 2) IA_SC(64, 1)
+#undef IA_SC
+  return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination");
+}
+
 }  // namespace ia
 
 extern "C" {

@@ -360,13 +360,69 @@ def paged_decode(q, pool_k, pool_v, block_table, seq_lens, *, max_seq_len=None, 
     return out
 
 
+FUSED_MAX_BLOCKS = 4096  # score rows the fused top-k decode stages in LDS
+FUSED_MAX_K_CAP = 512
+
+
 def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, block_size, forced_first=0,
-                       forced_last=0, forced_in_k=False, scale=None, scales=None, out=None, workspace=None):
-    """One decode-attention layer call of the top-k path: select, then finalize."""
-    idx, n_sel = select_blocks_topk(q, k_bar, seq_lens, k, block_size=block_size, forced_first=forced_first,
-                                    forced_last=forced_last, forced_in_k=forced_in_k, workspace=workspace)
-    return sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, block_size=block_size,
-                               scale=scale, scales=scales, out=out, workspace=workspace)
+                       forced_last=0, forced_in_k=False, k_cap=None, k_per_seq=None, scale=None, scales=None,
+                       out=None, out_dtype=None, return_selection=False, workspace=None):
+    """One decode-attention layer call of the top-k path: the selection of
+    ``select_blocks_topk`` followed by ``sparse_paged_decode``.  Up to 4096 blocks per
+    sequence and ``k_cap <= 512`` it runs fused (``ia_sparse_topk_decode``: a
+    many-workgroup scorer, then the finalize selecting in its prologue); beyond that
+    as the two calls.  With ``return_selection`` returns ``(out, idx, n_sel)``."""
+    _require_cuda(q, k_bar, seq_lens)
+    if k_bar.dim() != 4 or k_bar.stride(3) != 1 or k_bar.stride(2) != k_bar.shape[3]:
+        raise ValueError("k_bar must be [B, Hkv, nb_max, D] with contiguous blocks")
+    b, hkv, nb_max, d = (int(s_) for s_ in k_bar.shape)
+    if k < 0 or forced_first < 0 or forced_last < 0:
+        raise ValueError("k and forced block counts must be >= 0")
+    if k_per_seq is not None:
+        _require_cuda(k_per_seq)
+        _check_i32(k_per_seq, "k_per_seq", (b,))
+        if k_cap is None:
+            raise ValueError("k_per_seq needs an explicit k_cap")
+    if k_cap is None:
+        k_cap = max(int(k), forced_first + forced_last) if forced_in_k else int(k) + forced_first + forced_last
+    k_cap = max(int(k_cap), 1)
+    if nb_max > FUSED_MAX_BLOCKS or k_cap > FUSED_MAX_K_CAP:
+        idx, n_sel = select_blocks_topk(q, k_bar, seq_lens, k, block_size=block_size, forced_first=forced_first,
+                                        forced_last=forced_last, forced_in_k=forced_in_k, k_cap=k_cap,
+                                        k_per_seq=k_per_seq, workspace=workspace)
+        res = sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, block_size=block_size,
+                                  scale=scale, scales=scales, out=out, out_dtype=out_dtype, workspace=workspace)
+        return (res, idx, n_sel) if return_selection else res
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    if int(pool_k.shape[1]) != hkv or int(pool_k.shape[3]) != d:
+        raise ValueError("k_bar and the pool disagree on Hkv or head_dim")
+    sh = _decode_shape(q, hkv)
+    if q.shape[0] != b or q.shape[2] != d:
+        raise ValueError("q and k_bar disagree on batch or head_dim")
+    _check_i32(seq_lens, "seq_lens", (b,))
+    if block_table is not None and block_table.shape[0] != b:
+        raise ValueError("block_table rows must match the batch")
+    scale = d ** -0.5 if scale is None else float(scale)
+    out = _out_tensor(q, out, out_dtype, workspace)
+    dev = q.device
+    idx = n_sel = None
+    if return_selection:
+        idx = workspace_tensor(workspace, "topk_idx", (b, hkv, k_cap), device=dev, dtype=torch.int32)
+        n_sel = workspace_tensor(workspace, "topk_n_sel", (b, hkv), device=dev, dtype=torch.int32)
+    lib = N.lib()
+    g = int(q.shape[1]) // hkv
+    ws_bytes = lib.ia_sparse_topk_decode_workspace_size(b, hkv, g, d, nb_max, k_cap)
+    ws = _scratch(workspace if workspace is not None else {}, "topk_decode_scratch", ws_bytes, dev)
+    rc = lib.ia_sparse_topk_decode(
+        sh, q.data_ptr(), kv, seq_lens.data_ptr(), k_bar.data_ptr(), _code(k_bar.dtype, "k_bar"),
+        int(k_bar.stride(0)), int(k_bar.stride(1)), int(block_size), nb_max, int(k),
+        None if k_per_seq is None else k_per_seq.data_ptr(), int(forced_first), int(forced_last),
+        int(bool(forced_in_k)), k_cap, scale, out.data_ptr(), _code(out.dtype, "out"),
+        None if idx is None else idx.data_ptr(), None if n_sel is None else n_sel.data_ptr(), ws.data_ptr(),
+        ws.numel(), _stream(q))
+    N.check(rc)
+    del keep
+    return (out, idx, n_sel) if return_selection else out
 
 
 def nb_for(seq_len, block_size):

@@ -195,10 +195,13 @@ def test_fp8_paths_match_oracle(c, device):
     torch.cuda.synchronize()
     got, gd, gbf = out.float().cpu().numpy(), dense.float().cpu().numpy(), out_bf.float().cpu().numpy()
     for i, L in enumerate(lens):
-        ref = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], per_seq[i], block)
-        assert np.abs(got[i] - ref).max() <= 2e-3 + 2 ** -8 * np.abs(ref).max()
+        # Q.K is exact on the dequantised values; P.V uses bf16(p * v_scale) weights on the
+        # codes, within 2^-8 relative of the oracle's bf16(p) weights on dequantised V
+        vmax = float(np.abs(case["v"][i]).max())
+        ref = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], per_seq[i], block, p_bf16=True)
+        assert np.abs(got[i] - ref).max() <= 2e-3 + 2 ** -8 * vmax
         refd = A.dense_decode(case["q"][i], case["k"][i], case["v"][i])
-        assert np.abs(gd[i] - refd).max() <= 2e-3 + 2 ** -8 * np.abs(refd).max()
+        assert np.abs(gd[i] - refd).max() <= 2e-3 + 2 ** -8 * vmax
         assert np.abs(got[i] - gbf[i]).max() <= 6e-2
 
 
@@ -226,6 +229,30 @@ def test_fp8_codec_on_device(device):
     assert torch.equal(s["k_min"][0, 0, 0].cpu(), vals.min(0).values)
     # with max, min and the (exact) mean of the two non-zero codes per dim, every code is pinned
     assert torch.equal(s["k_bar"][0, 0, 0].cpu(), vals.sum(0) / page)
+
+
+def test_fp8_decode_widening_on_device(device):
+    """The finalize widens e4m3 codes to bf16 with v_cvt_scalef32_pk_bf16_fp8: with K = 0
+    every token weighs 1, so each output dim is the one non-zero V code / 16, exactly."""
+    if not hasattr(torch, "float8_e4m3fn"):
+        pytest.skip("torch without float8")
+    announce("fp8 decode widening")
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes = codes[(codes & 0x7F) != 0x7F]          # drop NaN codes: 254 codes
+    page, d = 16, 128
+    one = torch.ones((2, 1), device=device, dtype=torch.float32)
+    pool_v = torch.zeros((2, 1, page, d), dtype=torch.uint8)
+    pool_v[0, 0, 0, :] = codes[:d]
+    pool_v[1, 0, 0, :codes.numel() - d] = codes[d:]
+    pool_v = pool_v.to(device).view(torch.float8_e4m3fn)
+    pool_k = torch.zeros_like(pool_v)
+    q = torch.zeros((2, 1, d), device=device, dtype=torch.bfloat16)
+    table = torch.tensor([[0], [1]], device=device, dtype=torch.int32)
+    seq = torch.tensor([page, page], device=device, dtype=torch.int32)
+    out = ia.paged_decode(q, pool_k, pool_v, table, seq, max_seq_len=page, scales=(one, one), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    vals = pool_v[:, 0, 0, :].cpu().float()
+    assert torch.equal(out[:, 0].cpu(), vals / 16)
 
 
 def test_edge_cases(device):
@@ -309,3 +336,65 @@ def test_select_topk_long_rows_use_global_scores(return_scores, device):
             np.testing.assert_allclose(res[2][i, :, :nb].cpu().numpy(), sc[:, :nb], rtol=1e-5, atol=1e-5)
         for h in range(hkv):
             check_indices(idx[i, h], n_sel[i, h], sc[h, :nb], nb, 33, 2, 3, False)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_fused_topk_decode_equals_two_step(c, fp8, device):
+    """ia_sparse_topk_decode (scorer + finalize selecting in its prologue) returns the
+    same selection and the same output, bit for bit, as select_topk + sparse decode."""
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    if fp8 and dt == "f32":
+        pytest.skip("fp8 pools take bf16 q")
+    k, ff, fl, in_k = sel
+    announce(f"fused topk decode {name} fp8={fp8}")
+    case = _build(c, fp8=fp8)
+    dev = to_dev(case, device, _torch_dtype(dt), fp8=fp8)
+    nb_max = max(math.ceil(L / block) for L in lens) + 2
+    kb_dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max, k_bar_dtype=kb_dtype, scales=dev["scales"])
+    kw = dict(block_size=block, forced_first=ff, forced_last=fl, forced_in_k=in_k)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], summ["k_bar"], dev["seq_lens"], k, **kw)
+    ref = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block, scales=dev["scales"])
+    out, idx2, n_sel2 = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"],
+                                              dev["seq_lens"], summ["k_bar"], k, scales=dev["scales"],
+                                              return_selection=True, workspace={}, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(n_sel2, n_sel)
+    for i in range(b):
+        for h in range(hkv):
+            n = int(n_sel[i, h])
+            assert torch.equal(idx2[i, h, :n], idx[i, h, :n]), (i, h)
+    assert torch.equal(out, ref)
+
+
+def test_fused_topk_decode_k_per_seq_and_fallback(device):
+    """Per-sequence k (C3's rule) through the fused path, and the two-step fallback
+    past the fused limits (more than 4096 blocks)."""
+    announce("fused topk decode k_per_seq + fallback")
+    lens = [3000, 700, 1900]
+    case = make_case(seed=77, batch=3, hq=32, hkv=8, d=128, seq_lens=lens, page_size=16)
+    dev = to_dev(case, device)
+    block = 64
+    nb_max = max(math.ceil(L / block) for L in lens)
+    kvec = torch.tensor([max(2, math.ceil(L / block) // 8) for L in lens], device=device, dtype=torch.int32)
+    k_cap = int(kvec.max())
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], summ["k_bar"], dev["seq_lens"], 0, block_size=block,
+                                       k_per_seq=kvec, k_cap=k_cap)
+    ref = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block)
+    out = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                summ["k_bar"], 0, block_size=block, k_per_seq=kvec, k_cap=k_cap, workspace={})
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    # a k_bar row of more than 4096 blocks runs as the two calls
+    wide = torch.zeros((3, 8, 4100, 128), device=device, dtype=torch.bfloat16)
+    wide[:, :, :nb_max] = summ["k_bar"]
+    out2 = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                 wide, 0, block_size=block, k_per_seq=kvec, k_cap=k_cap, workspace={})
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref)

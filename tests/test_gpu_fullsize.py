@@ -1,0 +1,152 @@
+"""Parity at the BASELINE configs' full sizes (C3, C4, C5 shapes, one GPU).
+
+The oracle cannot run whole batches of 128K contexts in seconds, so the full-size
+checks use properties that do not depend on size, plus the oracle on a sample:
+* the fused layer call equals select + decode bit for bit (indices and output);
+* on sampled sequences, the selected blocks equal the oracle's top-k of the same
+  k_bar scores (near-tie rule) and the output equals exact attention over the
+  selected tokens (float64, 2e-2 abs: bf16 weights);
+* fp8 K/V (C5) stays within 6e-2 abs of the bf16 result on the same selection (the
+  stated fp8 tolerance);
+* the dense fallback over a whole 128K context equals float64 attention (2e-2).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import interattn_amd as ia
+from oracle import attention as A
+from oracle import select as S
+from tests._util import announce, check_indices
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D, PAGE = 32, 8, 128, 16
+
+
+def _make(device, lens, seed):
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    pages = [math.ceil(L / PAGE) for L in lens]
+    n_pages = sum(pages)
+    perm = torch.randperm(n_pages, device=device, generator=gen).to(torch.int32)
+    table = torch.full((len(lens), max(pages)), -1, device=device, dtype=torch.int32)
+    off = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = perm[off:off + n]
+        off += n
+    pool_k = torch.randn((n_pages, HKV, PAGE, D), device=device, dtype=torch.bfloat16, generator=gen)
+    pool_v = torch.randn((n_pages, HKV, PAGE, D), device=device, dtype=torch.bfloat16, generator=gen)
+    q = torch.randn((len(lens), HQ, D), device=device, dtype=torch.bfloat16, generator=gen)
+    seq = torch.tensor(lens, device=device, dtype=torch.int32)
+    return pool_k, pool_v, table, seq, q
+
+
+def _gather_head(pool, table_row, blocks, block, L, h):
+    """[tokens, D] float64 of the given logical blocks of one sequence and kv head."""
+    rows = []
+    for j in blocks:
+        lo, hi = j * block, min((j + 1) * block, L)
+        pg = table_row[lo // PAGE: (hi + PAGE - 1) // PAGE].long()
+        x = pool[pg, h].reshape(-1, D)[: hi - lo]
+        rows.append(x)
+    return torch.cat(rows).double().cpu().numpy()
+
+
+def _check_sample(q, pool_k, pool_v, table, seq, k_bar, idx, n_sel, out, block, k, sample, k_per_seq=None):
+    g = HQ // HKV
+    for b in sample:
+        L = int(seq[b])
+        nb = math.ceil(L / block)
+        counts = np.array([min(block, L - j * block) for j in range(nb)])
+        qb = q[b].double().cpu().numpy()
+        sc = S.topk_block_scores(qb, k_bar[b, :, :nb].double().cpu().numpy(), counts, g)
+        kb_ = int(k_per_seq[b]) if k_per_seq is not None else k
+        for h in range(HKV):
+            n = int(n_sel[b, h])
+            chosen = idx[b, h, :n].cpu().numpy()
+            check_indices(chosen, n, sc[h], nb, kb_, 0, 0, False)
+            kk = _gather_head(pool_k, table[b], chosen, block, L, h)
+            vv = _gather_head(pool_v, table[b], chosen, block, L, h)
+            ref = A.dense_decode(qb[h * g:(h + 1) * g], kk[None], vv[None])
+            got = out[b, h * g:(h + 1) * g].double().cpu().numpy()
+            assert np.abs(got - ref).max() <= 2e-2, (b, h)
+
+
+@pytest.fixture(scope="module")
+def c4(device):
+    announce("full-size C4 pool (16 x 131072, bf16)")
+    lens = [131072] * 16
+    pool_k, pool_v, table, seq, q = _make(device, lens, 1237)
+    summ = ia.build_block_summaries(pool_k, pool_v, table, seq, 128, nb_max=1024, k_bar_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    yield dict(pool_k=pool_k, pool_v=pool_v, table=table, seq=seq, q=q, k_bar=summ["k_bar"])
+
+
+def test_c4_fullsize(c4, device):
+    announce("C4 full size: fused == two-step, sampled oracle")
+    p = c4
+    out, idx, n_sel = ia.sparse_topk_decode(p["q"], p["pool_k"], p["pool_v"], p["table"], p["seq"], p["k_bar"], 64,
+                                            block_size=128, return_selection=True, workspace={})
+    idx2, n_sel2 = ia.select_blocks_topk(p["q"], p["k_bar"], p["seq"], 64, block_size=128)
+    out2 = ia.sparse_paged_decode(p["q"], p["pool_k"], p["pool_v"], p["table"], p["seq"], idx2, n_sel2,
+                                  block_size=128)
+    torch.cuda.synchronize()
+    assert torch.equal(n_sel, n_sel2) and torch.equal(idx, idx2) and torch.equal(out, out2)
+    assert bool((n_sel == 64).all())
+    _check_sample(p["q"], p["pool_k"], p["pool_v"], p["table"], p["seq"], p["k_bar"], idx, n_sel, out, 128, 64,
+                  sample=(0, 15))
+
+
+def test_c5_fullsize_fp8_vs_bf16(c4, device):
+    announce("C5 full size: fp8 K/V vs bf16 on the same selection")
+    p = c4
+    pk, pv = p["pool_k"], p["pool_v"]
+    ks = (pk.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
+    vs = (pv.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
+    k8 = (pk.float() / ks[:, :, None, None]).to(torch.float8_e4m3fn)
+    v8 = (pv.float() / vs[:, :, None, None]).to(torch.float8_e4m3fn)
+    idx, n_sel = ia.select_blocks_topk(p["q"], p["k_bar"], p["seq"], 64, block_size=128)
+    ref = ia.sparse_paged_decode(p["q"], pk, pv, p["table"], p["seq"], idx, n_sel, block_size=128)
+    got = ia.sparse_paged_decode(p["q"], k8, v8, p["table"], p["seq"], idx, n_sel, block_size=128, scales=(ks, vs))
+    torch.cuda.synchronize()
+    err = (got.float() - ref.float()).abs().max().item()
+    assert err <= 6e-2, err
+    del k8, v8
+
+
+def test_dense_fullsize_128k(c4, device):
+    announce("dense decode over 128K, two sequences")
+    p = c4
+    seq2 = p["seq"][:2].contiguous()
+    out = ia.paged_decode(p["q"][:2].contiguous(), p["pool_k"], p["pool_v"], p["table"][:2].contiguous(), seq2,
+                          max_seq_len=131072)
+    torch.cuda.synchronize()
+    b = 1
+    pg = p["table"][b].long()
+    kk = p["pool_k"][pg].permute(1, 0, 2, 3).reshape(HKV, -1, D).double().cpu().numpy()
+    vv = p["pool_v"][pg].permute(1, 0, 2, 3).reshape(HKV, -1, D).double().cpu().numpy()
+    ref = A.dense_decode(p["q"][b].double().cpu().numpy(), kk, vv)
+    assert np.abs(out[b].double().cpu().numpy() - ref).max() <= 2e-2
+
+
+def test_c3_fullsize_ragged(device):
+    announce("C3 full size: ragged batch, k = max(16, nb/16)")
+    lens = [int(x) for x in np.random.default_rng(1236).integers(8192, 65537, size=16)]
+    pool_k, pool_v, table, seq, q = _make(device, lens, 1236)
+    nb_max = max(math.ceil(L / 64) for L in lens)
+    summ = ia.build_block_summaries(pool_k, pool_v, table, seq, 64, nb_max=nb_max, k_bar_dtype=torch.bfloat16)
+    kvec = torch.tensor([max(16, math.ceil(L / 64) // 16) for L in lens], device=device, dtype=torch.int32)
+    k_cap = int(kvec.max())
+    out, idx, n_sel = ia.sparse_topk_decode(q, pool_k, pool_v, table, seq, summ["k_bar"], 0, block_size=64,
+                                            k_per_seq=kvec, k_cap=k_cap, return_selection=True, workspace={})
+    idx2, n_sel2 = ia.select_blocks_topk(q, summ["k_bar"], seq, 0, block_size=64, k_per_seq=kvec, k_cap=k_cap)
+    out2 = ia.sparse_paged_decode(q, pool_k, pool_v, table, seq, idx2, n_sel2, block_size=64)
+    torch.cuda.synchronize()
+    assert torch.equal(n_sel, n_sel2) and torch.equal(out, out2)
+    assert n_sel.cpu().tolist() == [[int(k)] * HKV for k in kvec.cpu().tolist()]
+    _check_sample(q, pool_k, pool_v, table, seq, summ["k_bar"], idx, n_sel, out, 64, 0, sample=(3, 11),
+                  k_per_seq=kvec.cpu().numpy())

@@ -12,6 +12,7 @@ CBT/core.py:558-570).
 """
 
 import math
+import os
 
 import torch
 
@@ -43,19 +44,31 @@ def _ensure_paged_layout(x, block_size):
     return x.contiguous()
 
 
-def summary_storage_dtypes(source_dtype, *, summary_dtype=torch.float32, mixed=False, k_bar_dtype=torch.float32):
+def summary_storage_dtypes(source_dtype, *, summary_dtype=None, mixed=None, k_bar_dtype=None):
     """Storage dtypes of (k_bar, v_bar, bounds): ``_summary_storage_dtypes``
-    (CBT/core.py:411-446) with explicit arguments instead of environment variables."""
+    (CBT/core.py:411-446).  Arguments left at None read the reference's switches
+    ``CONDITION_BLOCK_SUMMARY_DTYPE`` (default float32), ``CONDITION_BLOCK_MIXED_SUMMARIES``
+    and ``CONDITION_BLOCK_K_BAR_DTYPE`` (default float32); same ``ValueError``s."""
+    if summary_dtype is None:
+        name = os.environ.get("CONDITION_BLOCK_SUMMARY_DTYPE", "float32")
+        summary_dtype = getattr(torch, name)
+    if mixed is None:
+        mixed = os.environ.get("CONDITION_BLOCK_MIXED_SUMMARIES") == "1"
+    if k_bar_dtype is None:
+        name = os.environ.get("CONDITION_BLOCK_K_BAR_DTYPE", "float32")
+        if name not in ("float32", "bfloat16"):
+            raise ValueError(f"CONDITION_BLOCK_K_BAR_DTYPE must be float32 or bfloat16, got {name!r}.")
+        k_bar_dtype = getattr(torch, name)
     if k_bar_dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError(f"k_bar dtype must be float32 or bfloat16, got {k_bar_dtype!r}.")
+        raise ValueError(f"CONDITION_BLOCK_K_BAR_DTYPE must be float32 or bfloat16, got {k_bar_dtype!r}.")
     if not mixed and k_bar_dtype != torch.float32:
-        raise ValueError("a bfloat16 k_bar requires mixed summaries.")
+        raise ValueError("CONDITION_BLOCK_K_BAR_DTYPE=bfloat16 requires CONDITION_BLOCK_MIXED_SUMMARIES=1.")
     if not mixed:
         if summary_dtype not in (torch.float32, torch.bfloat16):
-            raise ValueError(f"summary dtype must be float32 or bfloat16, got {summary_dtype!r}.")
+            raise ValueError(f"summary dtype must be float32 or bfloat16 on this build, got {summary_dtype!r}.")
         return summary_dtype, summary_dtype, summary_dtype
     if summary_dtype != torch.float32:
-        raise ValueError("mixed summaries require a float32 summary dtype.")
+        raise ValueError("CONDITION_BLOCK_MIXED_SUMMARIES=1 requires CONDITION_BLOCK_SUMMARY_DTYPE=float32 (or unset).")
     bound = source_dtype if source_dtype in (torch.float32, torch.bfloat16) else torch.float32
     return k_bar_dtype, torch.bfloat16, bound
 
@@ -77,10 +90,12 @@ def _kv_desc(k_block, v_block, block_size):
     return kv
 
 
-def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=torch.float32, mixed=False,
-                         k_bar_dtype=torch.float32):
+def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=None, mixed=None, k_bar_dtype=None):
     """Prompt summaries (CBT/core.py:449-500): the same dict keys, built by the HIP
-    summary kernel over the padded block view."""
+    summary kernel over the padded block view.  Storage dtypes as
+    ``summary_storage_dtypes`` (keywords, else the reference's environment switches);
+    with ``CONDITION_BLOCK_TMA_BOUNDS=1`` the packed ``k_bounds [Hkv, nb, 2D]``
+    (k_max, k_min interleaved) is added as the reference does (CBT/core.py:490-499)."""
     _require_cuda(k_all, v_all)
     if block_size <= 0 or block_size % 16:
         raise ValueError("block_size must be a positive multiple of 16")
@@ -114,7 +129,7 @@ def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=torch.float3
             p(out["v_norm_max"]), p(out["v_norm_all"]), p(out["counts"]), _stream(k_all))
         N.check(rc)
     counts32 = out["counts"][0]
-    return {
+    res = {
         "k_block_attn": k_block,
         "v_block_attn": v_block,
         "token_idx": token_idx,
@@ -129,6 +144,9 @@ def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=torch.float3
         "_counts_i32": counts32,
         "_block_size": int(block_size),
     }
+    if os.environ.get("CONDITION_BLOCK_TMA_BOUNDS") == "1":
+        res["k_bounds"] = torch.stack((res["k_max"], res["k_min"]), dim=-1).flatten(2).contiguous()
+    return res
 
 
 def _summaries_desc(prefix, n_kv_heads, head_dim):

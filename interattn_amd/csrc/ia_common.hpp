@@ -54,6 +54,21 @@ __device__ __forceinline__ u32 fp8x2_to_bf16x2(u32 w) {
   return __builtin_bit_cast(u32, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
 }
 
+// ------------------------------------------------------------------ MFMA operands
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;  // 16x16x32 bf16 A/B operand
+typedef __attribute__((ext_vector_type(4))) short i16x4_t;    // 16x16x16 bf16 A/B operand
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;    // 16x16 f32 accumulator
+typedef __attribute__((ext_vector_type(4))) u32 u32x4_t;
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const u32* w) {
+  return __builtin_bit_cast(bf16x8_t, u32x4_t{w[0], w[1], w[2], w[3]});
+}
+__device__ __forceinline__ i16x4_t as_i16x4(u32 lo, u32 hi) {
+  typedef __attribute__((ext_vector_type(2))) u32 u32x2_t;
+  return __builtin_bit_cast(i16x4_t, u32x2_t{lo, hi});
+}
+
 // ------------------------------------------------------------------ DPP within 16-lane rows
 
 constexpr int kDppRowMirror = 0x140;

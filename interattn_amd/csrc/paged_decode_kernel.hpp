@@ -15,23 +15,28 @@
 //   partials.
 //   There is no cross-workgroup synchronisation inside a launch.
 //
-// Lane layout (head_dim D, DPL = D/16 dims per lane)
-//   lane = 16*r + c.  A subtile is read as four steps i = 0..3; in step i, row
-//   r holds token 4i + r and lane c holds dims [c*DPL, (c+1)*DPL): one
-//   contiguous 4-token load per wave per step (1 KiB for bf16 D=128).  K and V
-//   of the next subtiles are in flight in a ring of register buffers while the
-//   current one is consumed (two subtiles, 16 KiB per wave, for bf16).  Q.K
-//   partial sums for the 4 steps x G query rows are
-//   reduce-scattered over the 16-lane row with DPP, leaving each lane the
-//   complete score of one (token, query row) pair; the softmax weights reach
-//   the V lanes of the same row through DPP row broadcasts (row_newbcast).
+// Lane layout (head_dim D, DPL = D/16 dims per lane; lane = 16*r + c)
+//   K and V of the next subtiles are in flight in a ring of register buffers
+//   while the current one is consumed (two subtiles, 16 KiB per wave, for bf16).
+//   bf16 and fp8 caches (MFMA): V is read as four steps i = 0..3, row r holding
+//   token 4i + r and lane c dims [c*DPL, (c+1)*DPL); K is read as 16-byte pieces,
+//   lane c taking token c/4 + 4 (c%4).  Q.K runs as v_mfma_f32_16x16x32_bf16 with
+//   the G query rows replicated over the 16 columns, which leaves each lane the
+//   scores of tokens r, r+4, r+8, r+12 for query row c % G: exactly the k-slice
+//   of the P operand of the P.V product (v_mfma_f32_16x16x16_bf16, one per dim
+//   group), whose V operand is the lane's own four row loads interleaved by
+//   v_perm.  fp8 codes are widened to bf16 in registers (exact).
+//   fp32 caches (VALU): the same V layout for K; Q.K partial sums for the 4 steps
+//   x G query rows are reduce-scattered over the 16-lane row with DPP, leaving
+//   each lane the complete score of one (token, query row) pair; the softmax
+//   weights reach the V lanes of the same row through DPP row broadcasts.
 //
 // Numerics follow the reference's fused kernel (CBT/page_attention.py):
-//   bf16 K/V: scores = bf16(q) . K in fp32 (v_dot2_f32_bf16), fp32 online
-//   softmax, weights rounded to bf16 for the P.V product (:248-252), fp32
-//   normaliser (:253).  fp32 K/V: everything in fp32.  fp8 K/V: codes are
-//   widened to fp32, the per-(page, head) scale multiplies the score and the
-//   weight.
+//   bf16 K/V: scores = bf16(q) . K accumulated in fp32, fp32 online softmax,
+//   weights rounded to bf16 for the P.V product (:248-252), fp32 normaliser
+//   (:253).  fp32 K/V: everything in fp32.  fp8 K/V: as bf16 on the widened
+//   codes; the per-(page, head) scale multiplies the score and is folded into
+//   the weight before its bf16 rounding.
 #pragma once
 
 #include "topk_select.hpp"
@@ -215,8 +220,35 @@ struct WeightBcast<G, 0> {
   __device__ __forceinline__ static void run(const float*, float (*)[G]) {}
 };
 
+// First of the 8 dims that lane row r (lane / 16) feeds into k-slice kk of the Q.K
+// MFMA.  K is read in 16-byte pieces at byte 64*pc + 16*r of the token row: 8 bf16
+// dims per piece (one k-slice) or 16 e4m3 dims (two k-slices).  Q is loaded at the
+// same dims, so the order of dims inside the dot product is the only change.
+template <int KBYTES>
+__device__ __forceinline__ int mfma_kslice(int kk, int r) {
+  return KBYTES == 2 ? 32 * kk + 8 * r : 64 * (kk >> 1) + 16 * r + 8 * (kk & 1);
+}
+
+// Softmax rescale factor of accumulator row i of lane row r (query row (4r + i) % G)
+// from a lane that owns that query row: quad lane i of the same quad for G | 4
+// (quad_perm [i,i,i,i]), lane 4 (r & 1) + i of the same lane row for G = 8.
+template <int G>
+__device__ __forceinline__ float mfma_row_alpha(float alpha, int i, int lane) {
+  if constexpr (G == 8) {
+    return __shfl(alpha, (lane & 48) + 4 * ((lane >> 4) & 1) + i, 64);
+  } else {
+    const int a = __float_as_int(alpha);
+    switch (i) {
+      case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(a, 0x00, 0xf, 0xf, false));
+      case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(a, 0x55, 0xf, 0xf, false));
+      case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(a, 0xAA, 0xf, 0xf, false));
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(a, 0xFF, 0xf, 0xf, false));
+    }
+  }
+}
+
 template <int D, int G, typename KV, int SRC>
-__global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(DecodeParams p) {
+__global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
   constexpr int NWD = DPL * KV::kBytes / 4;
   using SM = ScoreMap<G>;
@@ -228,6 +260,9 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   // P.V as bf16 pairs through v_dot2_f32_bf16; fp32 caches stay fp32
   constexpr bool kDot2 = kBf16 || kFp8;
   constexpr int NWB = DPL / 2;  // bf16 words per lane per token row
+  // bf16 / fp8 caches: Q.K and P.V on MFMA (query rows padded to the 16-row tile)
+  constexpr bool kMfma = kDot2;
+  constexpr int kMfmaK = D / 32;  // 32-dim k-slices of Q.K
 
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
@@ -252,25 +287,28 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   const int b = blockIdx.z;
   const int bh = b * p.n_kv_heads + h;
 
-  // ---- query rows of this kv head, in the lane's dim slice: raw loads issued first
-  // (independent of the prologue), converted after it
-  u32 qraw[G][DPL];  // f32 q: DPL floats; bf16 q: DPL/2 pairs
-  {
-    const int d0 = c16 * DPL;
+  // ---- query rows of this kv head: raw loads issued first (independent of the
+  // prologue), converted after it.  Vector path: every row at the lane's dim slice
+  // c16*DPL ..; MFMA path: row c16 % G at the dims of the lane's k-slices.
+  constexpr int QR0 = kMfma ? kMfmaK : G;
+  constexpr int QR1 = kMfma ? 8 : DPL;
+  u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs (upper half unused)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
-      if (p.q_f32) {
-        const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
+  for (int x = 0; x < QR0; ++x) {
+    const int g = kMfma ? c16 % G : x;
+    const int d0 = kMfma ? mfma_kslice<KV::kBytes>(x, r) : c16 * DPL;
+    constexpr int NE = kMfma ? 8 : DPL;
+    const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
+    if (p.q_f32) {
+      const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) qraw[g][e] = qp[e];
-      } else {
-        const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
+      for (int e = 0; e < NE; ++e) qraw[x][e] = qp[e];
+    } else {
+      const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
 #pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) qraw[g][e] = (u32)qp[2 * e] | ((u32)qp[2 * e + 1] << 16);
+      for (int e = 0; e < NE / 2; ++e) qraw[x][e] = (u32)qp[2 * e] | ((u32)qp[2 * e + 1] << 16);
 #pragma unroll
-        for (int e = DPL / 2; e < DPL; ++e) qraw[g][e] = 0u;
-      }
+      for (int e = NE / 2; e < QR1; ++e) qraw[x][e] = 0u;
     }
   }
 
@@ -431,61 +469,9 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
 
   __syncthreads();
 
-  constexpr int QW = kDot2 ? DPL / 2 : DPL;  // bf16 pairs or floats
-  u32 qw[G][QW];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (p.q_f32) {
-      if constexpr (kDot2) {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e)
-          qw[g][e] = pack_bf16x2(__uint_as_float(qraw[g][2 * e]), __uint_as_float(qraw[g][2 * e + 1]));
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) qw[g][e] = qraw[g][e];
-      }
-    } else {
-      if constexpr (kDot2) {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) qw[g][e] = qraw[g][e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < DPL / 2; ++e) {
-          qw[g][2 * e] = __float_as_uint(bf16_lo(qraw[g][e]));
-          qw[g][2 * e + 1] = __float_as_uint(bf16_hi(qraw[g][e]));
-        }
-      }
-    }
-  }
-
   const char* kbase = reinterpret_cast<const char*>(kv.k) + (int64_t)h * kv.k_head_stride * KV::kBytes;
   const char* vbase = reinterpret_cast<const char*>(kv.v) + (int64_t)h * kv.v_head_stride * KV::kBytes;
   const int lane_off = c16 * DPL * KV::kBytes;
-
-  // Per-lane ownership of reduce-scattered scores: token step and query rows.
-  const int my_step = c16 >> 2;
-  int my_g[KG];
-#pragma unroll
-  for (int k = 0; k < KG; ++k) {
-    if constexpr (G == 8) my_g[k] = 2 * (c16 & 3) + k;
-    else if constexpr (G == 4) my_g[k] = c16 & 3;
-    else if constexpr (G == 2) my_g[k] = (c16 >> 1) & 1;
-    else my_g[k] = 0;
-  }
-  // For G < 4 several lanes hold copies of one score; only one copy counts in l.
-  const bool l_owner = (G >= 4) || ((c16 & (G == 2 ? 1 : 3)) == 0);
-
-  float m_run[KG], l_run[KG];
-#pragma unroll
-  for (int k = 0; k < KG; ++k) {
-    m_run[k] = kNegInf;
-    l_run[k] = 0.f;
-  }
-  float acc[G][DPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
 
   // ---- subtile iterator: wave w takes the item's valid subtiles w, w + 4, ...
   struct Sub {
@@ -501,11 +487,8 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
   };
   auto next = [&](const Sub& c) -> Sub { return seek(c.k + kWaves); };
 
-  auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
-    if (sb.k >= n_sub) return;
-    const char* kp;
-    const char* vp;
-    int64_t kts, vts;  // row strides in bytes
+  // K and V row pointers of a subtile and their row strides in bytes
+  auto sub_rows = [&](const Sub& sb, const char*& kp, const char*& vp, int64_t& kts, int64_t& vts) {
     if (SRC == kSrcLists && sb.pg == kSfxPage) {
       kts = p.sfx_k_token_stride * KV::kBytes;
       vts = p.sfx_v_token_stride * KV::kBytes;
@@ -519,187 +502,403 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_paged_finalize(De
       kp = kbase + (int64_t)sb.pg * kv.k_page_stride * KV::kBytes + (int64_t)sb.row * kts;
       vp = vbase + (int64_t)sb.pg * kv.v_page_stride * KV::kBytes + (int64_t)sb.row * vts;
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // rows past the subtile's valid rows re-read its first row (always valid); their weights are zero
-      const int tl = (4 * i + r < sb.nv) ? 4 * i + r : 0;
-      load_words<NWD>(kp + (int64_t)tl * kts + lane_off, kb[i]);
-      load_words<NWD>(vp + (int64_t)tl * vts + lane_off, vb[i]);
-    }
-  };
-
-  auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
-    // fp8 rows widened to bf16 pairs (exact: every e4m3 value is a bf16 value)
-    u32 kx[4][NWB], vx[4][NWB];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (kFp8) {
-#pragma unroll
-        for (int w = 0; w < NWD; ++w) {
-          kx[i][2 * w] = fp8x2_to_bf16x2<false>(kb[i][w]);
-          kx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(kb[i][w]);
-          vx[i][2 * w] = fp8x2_to_bf16x2<false>(vb[i][w]);
-          vx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(vb[i][w]);
-        }
-      } else if constexpr (kBf16) {
-#pragma unroll
-        for (int w = 0; w < NWB; ++w) {
-          kx[i][w] = kb[i][w];
-          vx[i][w] = vb[i][w];
-        }
-      }
-    }
-    // ---------------- scores of the 16 tokens x G rows
-    float part[NV];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (kDot2) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float a = 0.f;
-#pragma unroll
-          for (int w = 0; w < NWB; ++w)
-            a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kx[i][w]), a, false);
-          part[i * G + g] = a;
-        }
-      } else {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float a = 0.f;
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), __uint_as_float(kb[i][e]), a);
-          part[i * G + g] = a;
-        }
-      }
-    }
-    reduce_scatter16<NV>(part, lane);
-    float sc = p.scale_log2;
-    float vsc = 1.f;
-    if constexpr (kFp8) {
-      if (sb.pg >= 0) {
-        sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
-        vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
-      }
-    }
-    const bool valid = 4 * my_step + r < sb.nv;
-
-    // ---------------- online softmax, one update per subtile
-    float pw[KG], m_new[KG];
-    bool grow = false;
-#pragma unroll
-    for (int k = 0; k < KG; ++k) {
-      const float sv = valid ? part[k] * sc : kNegInf;
-      const float mt = fold_g<G, true>(sv);
-      m_new[k] = fmaxf(m_run[k], mt);
-      grow |= m_new[k] > m_run[k];
-      pw[k] = (sv == kNegInf) ? 0.f : exp2f(sv - m_new[k]);
-    }
-    if (__any(grow)) {
-      float alpha[KG];
-#pragma unroll
-      for (int k = 0; k < KG; ++k) {
-        alpha[k] = (m_new[k] == kNegInf) ? 1.f : exp2f(m_run[k] - m_new[k]);
-        l_run[k] *= alpha[k];
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float a = alpha_of_row<G>(alpha, g);
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[g][e] *= a;
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < KG; ++k) {
-      m_run[k] = m_new[k];
-      l_run[k] += l_owner ? pw[k] : 0.f;
-    }
-
-    // ---------------- weighted values: weight of (token 4i + r, g) by row broadcast
-    float pb[4][G];
-    WeightBcast<G, 4 * G>::run(pw, pb);
-    if constexpr (kDot2) {
-      // bf16 weights (the reference's cast point); an fp8 page's V scale is folded
-      // into the weight before the rounding
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) {
-        const int i1 = 2 * pr, i2 = 2 * pr + 1;
-        u32 pp[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) pp[g] = kFp8 ? pack_bf16x2(pb[i1][g] * vsc, pb[i2][g] * vsc)
-                                                 : pack_bf16x2(pb[i1][g], pb[i2][g]);
-#pragma unroll
-        for (int w = 0; w < NWB; ++w) {
-          const u32 lo = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x05040100u);
-          const u32 hi = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x07060302u);
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            acc[g][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(lo), acc[g][2 * w], false);
-            acc[g][2 * w + 1] =
-                __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(hi), acc[g][2 * w + 1], false);
-          }
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pb[i][g], __uint_as_float(vb[i][e]), acc[g][e]);
-    }
   };
 
   // ---- software pipeline over a ring of NBUF register buffers: while subtile n
   // is consumed, subtiles n+1 .. n+NBUF-1 are in flight
-  constexpr int NBUF = KV::kRing;
-  u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD];
-  Sub ring[NBUF];
-  ring[0] = seek(wave);
-  issue(ring[0], kbuf[0], vbuf[0]);
+  auto stream = [&](auto&& issue, auto&& consume) {
+    constexpr int NBUF = KV::kRing;
+    u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD];
+    Sub ring[NBUF];
+    ring[0] = seek(wave);
+    issue(ring[0], kbuf[0], vbuf[0]);
 #pragma unroll
-  for (int k = 1; k < NBUF - 1; ++k) {
-    ring[k] = next(ring[k - 1]);
-    issue(ring[k], kbuf[k], vbuf[k]);
-  }
-  bool done = false;
-  while (!done) {
+    for (int k = 1; k < NBUF - 1; ++k) {
+      ring[k] = next(ring[k - 1]);
+      issue(ring[k], kbuf[k], vbuf[k]);
+    }
+    bool done = false;
+    while (!done) {
 #pragma unroll
-    for (int k = 0; k < NBUF; ++k) {
-      const int fk = (k + NBUF - 1) % NBUF;  // free buffer
-      const int pk = (k + NBUF - 2) % NBUF;  // most recently issued
-      if (ring[k].k >= n_sub) {
-        done = true;
-        break;
+      for (int k = 0; k < NBUF; ++k) {
+        const int fk = (k + NBUF - 1) % NBUF;  // free buffer
+        const int pk = (k + NBUF - 2) % NBUF;  // most recently issued
+        if (ring[k].k >= n_sub) {
+          done = true;
+          break;
+        }
+        ring[fk] = next(ring[pk]);
+        issue(ring[fk], kbuf[fk], vbuf[fk]);
+        consume(ring[k], kbuf[k], vbuf[k]);
       }
-      ring[fk] = next(ring[pk]);
-      issue(ring[fk], kbuf[fk], vbuf[fk]);
-      consume(ring[k], kbuf[k], vbuf[k]);
     }
-  }
+  };
 
-  // ---- fold the wave: rows (xor 16, 32) for acc, g-sharing lanes for l
+  if constexpr (kMfma) {
+    // ================= bf16 / fp8 caches: both products on MFMA, one subtile at a time
+    // Q.K: S^T = K Q^T with v_mfma_f32_16x16x32_bf16 per 32-dim k-slice.  A = the 16
+    // token rows (lane (r, c16) feeds A row c16 with token rho = c16/4 + 4 (c16%4) of
+    // the subtile, 8 dims of k-slice kk at mfma_kslice(kk, r)); B = the G query rows
+    // replicated over the 16 columns (column c <-> query row c % G).  Accumulator i
+    // of lane (r, c16) then holds the score of token r + 4i for query row c16 % G.
+    // P.V: O += P V with v_mfma_f32_16x16x16_bf16 per dim group n < DPL.  A = P: row
+    // c16 (query row c16 % G), k = 4r + i <-> token r + 4i, i.e. the lane's own four
+    // weights; B = V: column c16 <-> dim c16*DPL + n, k = 4r + i <-> token 4i + r, the
+    // lane's own row loads of steps i = 0..3 interleaved by v_perm.  Accumulator i of
+    // lane (r, c16) holds O[row 4r + i][dim c16*DPL + n], row 4r + i <-> query row
+    // (4r + i) % G.  Scores and weights never leave the lane.
+    const int rho = (c16 >> 2) + 4 * (c16 & 3);
+    u32 qop[kMfmaK][4];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+    for (int kk = 0; kk < kMfmaK; ++kk)
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      float v = acc[g][e];
-      v += shfl_xor_f(v, 16);
-      v += shfl_xor_f(v, 32);
-      acc[g][e] = v;
+      for (int e = 0; e < 4; ++e)
+        qop[kk][e] = p.q_f32 ? pack_bf16x2(__uint_as_float(qraw[kk][2 * e]), __uint_as_float(qraw[kk][2 * e + 1]))
+                             : qraw[kk][e];
+    f32x4_t acc[DPL];
+#pragma unroll
+    for (int n = 0; n < DPL; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegInf, l_run = 0.f;
+
+    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
+      if (sb.k >= n_sub) return;
+      const char* kp;
+      const char* vp;
+      int64_t kts, vts;
+      sub_rows(sb, kp, vp, kts, vts);
+      // K: token rho (row 0 past the valid rows), NWD 16-byte pieces at 64*pc + 16*r
+      const char* kr = kp + (int64_t)(rho < sb.nv ? rho : 0) * kts + 16 * r;
+#pragma unroll
+      for (int pc = 0; pc < NWD; ++pc) {
+        const uint4 a = *reinterpret_cast<const uint4*>(kr + 64 * pc);
+        const u32 w4[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kb[(4 * pc + e) / NWD][(4 * pc + e) % NWD] = w4[e];
+      }
+      // V: step i, token 4i + r, dims c16*DPL ..
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tl = (4 * i + r < sb.nv) ? 4 * i + r : 0;
+        load_words<NWD>(vp + (int64_t)tl * vts + lane_off, vb[i]);
+      }
+    };
+
+    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+      auto kword = [&](int fw) -> u32 { return kb[fw / NWD][fw % NWD]; };
+      // ---------------- scores: token r + 4i, query row c16 % G, in accumulator i
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < kMfmaK; ++kk) {
+        u32 w[4];
+        if constexpr (kFp8) {  // piece kk/2, half kk%2: 8 codes widened to bf16 (exact)
+          const u32 c0 = kword(4 * (kk >> 1) + 2 * (kk & 1)), c1 = kword(4 * (kk >> 1) + 2 * (kk & 1) + 1);
+          w[0] = fp8x2_to_bf16x2<false>(c0);
+          w[1] = fp8x2_to_bf16x2<true>(c0);
+          w[2] = fp8x2_to_bf16x2<false>(c1);
+          w[3] = fp8x2_to_bf16x2<true>(c1);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = kword(4 * kk + e);
+        }
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(w), as_bf16x8(qop[kk]), s, 0, 0, 0);
+      }
+      float sc = p.scale_log2;
+      float vsc = 1.f;
+      if constexpr (kFp8) {
+        if (sb.pg >= 0) {
+          sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+          vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+        }
+      }
+      // ---------------- online softmax, one update per subtile (max over the 16
+      // tokens: in-lane over i, then over the four lane rows)
+      float sv[4];
+      float mt = kNegInf;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[i] = (r + 4 * i < sb.nv) ? s[i] * sc : kNegInf;
+        mt = fmaxf(mt, sv[i]);
+      }
+      mt = fmaxf(mt, shfl_xor_f(mt, 16));
+      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      const float m_new = fmaxf(m_run, mt);
+      float pw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pw[i] = (sv[i] == kNegInf) ? 0.f : exp2f(sv[i] - m_new);
+      if (__any(m_new > m_run)) {
+        const float alpha = (m_new == kNegInf) ? 1.f : exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = mfma_row_alpha<G>(alpha, i, lane);
+#pragma unroll
+          for (int n = 0; n < DPL; ++n) acc[n][i] *= a;
+        }
+      }
+      m_run = m_new;
+      l_run += (pw[0] + pw[1]) + (pw[2] + pw[3]);
+      // ---------------- weighted values: bf16 weights (the reference's cast point);
+      // an fp8 page's V scale is folded into the weight before the rounding
+      const u32 pa0 = kFp8 ? pack_bf16x2(pw[0] * vsc, pw[1] * vsc) : pack_bf16x2(pw[0], pw[1]);
+      const u32 pa1 = kFp8 ? pack_bf16x2(pw[2] * vsc, pw[3] * vsc) : pack_bf16x2(pw[2], pw[3]);
+      const i16x4_t pa = as_i16x4(pa0, pa1);
+      u32 vx[4][NWB];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (kFp8) {
+#pragma unroll
+          for (int w = 0; w < NWD; ++w) {
+            vx[i][2 * w] = fp8x2_to_bf16x2<false>(vb[i][w]);
+            vx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(vb[i][w]);
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < NWB; ++w) vx[i][w] = vb[i][w];
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < DPL; ++n) {
+        const u32 sel = (n & 1) ? 0x07060302u : 0x05040100u;
+        const u32 b0 = __builtin_amdgcn_perm(vx[1][n >> 1], vx[0][n >> 1], sel);
+        const u32 b1 = __builtin_amdgcn_perm(vx[3][n >> 1], vx[2][n >> 1], sel);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, as_i16x4(b0, b1), acc[n], 0, 0, 0);
+      }
+    };
+
+    stream(issue, consume);
+
+    // ---- fold the wave: l over the four lane rows; the query rows' accumulators sit
+    // in lane rows r < max(1, G/4) (row 4r + i < G)
+    l_run += shfl_xor_f(l_run, 16);
+    l_run += shfl_xor_f(l_run, 32);
+    if (r == 0 && c16 < G) {
+      wm_lds[wave][c16] = m_run;
+      wl_lds[wave][c16] = l_run;
     }
 #pragma unroll
-  for (int k = 0; k < KG; ++k) l_run[k] = fold_g<G, false>(l_run[k]);
-  if (r == 0) {
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * r + i;
+      if (row < G) {
+#pragma unroll
+        for (int n = 0; n < DPL; ++n) wacc_lds[wave][row * D + c16 * DPL + n] = acc[n][i];
+      }
+    }
+  } else {
+
+    constexpr int QW = kDot2 ? DPL / 2 : DPL;  // bf16 pairs or floats
+    u32 qw[G][QW];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (p.q_f32) {
+        if constexpr (kDot2) {
+#pragma unroll
+          for (int e = 0; e < DPL / 2; ++e)
+            qw[g][e] = pack_bf16x2(__uint_as_float(qraw[g][2 * e]), __uint_as_float(qraw[g][2 * e + 1]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) qw[g][e] = qraw[g][e];
+        }
+      } else {
+        if constexpr (kDot2) {
+#pragma unroll
+          for (int e = 0; e < DPL / 2; ++e) qw[g][e] = qraw[g][e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < DPL / 2; ++e) {
+            qw[g][2 * e] = __float_as_uint(bf16_lo(qraw[g][e]));
+            qw[g][2 * e + 1] = __float_as_uint(bf16_hi(qraw[g][e]));
+          }
+        }
+      }
+    }
+
+    // Per-lane ownership of reduce-scattered scores: token step and query rows.
+    const int my_step = c16 >> 2;
+    int my_g[KG];
+#pragma unroll
+    for (int k = 0; k < KG; ++k) {
+      if constexpr (G == 8) my_g[k] = 2 * (c16 & 3) + k;
+      else if constexpr (G == 4) my_g[k] = c16 & 3;
+      else if constexpr (G == 2) my_g[k] = (c16 >> 1) & 1;
+      else my_g[k] = 0;
+    }
+    // For G < 4 several lanes hold copies of one score; only one copy counts in l.
+    const bool l_owner = (G >= 4) || ((c16 & (G == 2 ? 1 : 3)) == 0);
+
+    float m_run[KG], l_run[KG];
+#pragma unroll
+    for (int k = 0; k < KG; ++k) {
+      m_run[k] = kNegInf;
+      l_run[k] = 0.f;
+    }
+    float acc[G][DPL];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) wacc_lds[wave][g * D + c16 * DPL + e] = acc[g][e];
-  }
-  if (r == 0 && c16 < 4) {
+      for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
+
+    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
+      if (sb.k >= n_sub) return;
+      const char* kp;
+      const char* vp;
+      int64_t kts, vts;
+      sub_rows(sb, kp, vp, kts, vts);
 #pragma unroll
-    for (int k = 0; k < KG; ++k) {
-      wm_lds[wave][my_g[k]] = m_run[k];
-      wl_lds[wave][my_g[k]] = l_run[k];
+      for (int i = 0; i < 4; ++i) {
+        // rows past the subtile's valid rows re-read its first row (always valid); their weights are zero
+        const int tl = (4 * i + r < sb.nv) ? 4 * i + r : 0;
+        load_words<NWD>(kp + (int64_t)tl * kts + lane_off, kb[i]);
+        load_words<NWD>(vp + (int64_t)tl * vts + lane_off, vb[i]);
+      }
+    };
+
+    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+      // fp8 rows widened to bf16 pairs (exact: every e4m3 value is a bf16 value)
+      u32 kx[4][NWB], vx[4][NWB];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (kFp8) {
+#pragma unroll
+          for (int w = 0; w < NWD; ++w) {
+            kx[i][2 * w] = fp8x2_to_bf16x2<false>(kb[i][w]);
+            kx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(kb[i][w]);
+            vx[i][2 * w] = fp8x2_to_bf16x2<false>(vb[i][w]);
+            vx[i][2 * w + 1] = fp8x2_to_bf16x2<true>(vb[i][w]);
+          }
+        } else if constexpr (kBf16) {
+#pragma unroll
+          for (int w = 0; w < NWB; ++w) {
+            kx[i][w] = kb[i][w];
+            vx[i][w] = vb[i][w];
+          }
+        }
+      }
+      // ---------------- scores of the 16 tokens x G rows
+      float part[NV];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (kDot2) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float a = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWB; ++w)
+              a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kx[i][w]), a, false);
+            part[i * G + g] = a;
+          }
+        } else {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            float a = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), __uint_as_float(kb[i][e]), a);
+            part[i * G + g] = a;
+          }
+        }
+      }
+      reduce_scatter16<NV>(part, lane);
+      float sc = p.scale_log2;
+      float vsc = 1.f;
+      if constexpr (kFp8) {
+        if (sb.pg >= 0) {
+          sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+          vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+        }
+      }
+      const bool valid = 4 * my_step + r < sb.nv;
+
+      // ---------------- online softmax, one update per subtile
+      float pw[KG], m_new[KG];
+      bool grow = false;
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        const float sv = valid ? part[k] * sc : kNegInf;
+        const float mt = fold_g<G, true>(sv);
+        m_new[k] = fmaxf(m_run[k], mt);
+        grow |= m_new[k] > m_run[k];
+        pw[k] = (sv == kNegInf) ? 0.f : exp2f(sv - m_new[k]);
+      }
+      if (__any(grow)) {
+        float alpha[KG];
+#pragma unroll
+        for (int k = 0; k < KG; ++k) {
+          alpha[k] = (m_new[k] == kNegInf) ? 1.f : exp2f(m_run[k] - m_new[k]);
+          l_run[k] *= alpha[k];
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float a = alpha_of_row<G>(alpha, g);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[g][e] *= a;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        m_run[k] = m_new[k];
+        l_run[k] += l_owner ? pw[k] : 0.f;
+      }
+
+      // ---------------- weighted values: weight of (token 4i + r, g) by row broadcast
+      float pb[4][G];
+      WeightBcast<G, 4 * G>::run(pw, pb);
+      if constexpr (kDot2) {
+        // bf16 weights (the reference's cast point); an fp8 page's V scale is folded
+        // into the weight before the rounding
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          const int i1 = 2 * pr, i2 = 2 * pr + 1;
+          u32 pp[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) pp[g] = kFp8 ? pack_bf16x2(pb[i1][g] * vsc, pb[i2][g] * vsc)
+                                                   : pack_bf16x2(pb[i1][g], pb[i2][g]);
+#pragma unroll
+          for (int w = 0; w < NWB; ++w) {
+            const u32 lo = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x05040100u);
+            const u32 hi = __builtin_amdgcn_perm(vx[i2][w], vx[i1][w], 0x07060302u);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              acc[g][2 * w] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(lo), acc[g][2 * w], false);
+              acc[g][2 * w + 1] =
+                  __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pp[g]), as_bf16x2(hi), acc[g][2 * w + 1], false);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[g][e] = fmaf(pb[i][g], __uint_as_float(vb[i][e]), acc[g][e]);
+      }
+    };
+
+    stream(issue, consume);
+
+    // ---- fold the wave: rows (xor 16, 32) for acc, g-sharing lanes for l
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        float v = acc[g][e];
+        v += shfl_xor_f(v, 16);
+        v += shfl_xor_f(v, 32);
+        acc[g][e] = v;
+      }
+#pragma unroll
+    for (int k = 0; k < KG; ++k) l_run[k] = fold_g<G, false>(l_run[k]);
+    if (r == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) wacc_lds[wave][g * D + c16 * DPL + e] = acc[g][e];
+    }
+    if (r == 0 && c16 < 4) {
+#pragma unroll
+      for (int k = 0; k < KG; ++k) {
+        wm_lds[wave][my_g[k]] = m_run[k];
+        wl_lds[wave][my_g[k]] = l_run[k];
+      }
     }
   }
   __syncthreads();

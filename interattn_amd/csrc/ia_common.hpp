@@ -83,6 +83,23 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+constexpr int kDppRowShr1 = 0x111;     // row_shr:n = 0x110 + n
+constexpr int kDppRowBcast15 = 0x142;  // lane 15 of each row to the next row
+constexpr int kDppRowBcast31 = 0x143;  // lane 31 to rows 2 and 3
+
+// Inclusive prefix sum over the 64 lanes in lane order, all in DPP (no LDS):
+// row_shr 1, 2, 4, 8 scan each 16-lane row, then the row totals are carried by
+// row_bcast15 (rows 1, 3) and row_bcast31 (rows 2, 3).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1 + 1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1 + 3, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowShr1 + 7, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast15, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppRowBcast31, 0xc, 0xf, false);
+  return v;
+}
+
 // Sum over the 16 lanes of a row; every lane receives the total.  Partner sets
 // of mirror, half-mirror, xor2, xor1 are disjoint at each step.
 __device__ __forceinline__ float row16_sum(float v) {

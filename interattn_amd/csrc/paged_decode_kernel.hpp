@@ -2,13 +2,13 @@
 // the dense fallback share one kernel template.
 //
 // Work decomposition
-//   grid = (items, Hkv, batch); one 256-thread workgroup (4 waves) per split-K
+//   grid = (items, Hkv, batch); one 512-thread workgroup (8 waves) per split-K
 //   item of one (sequence, kv head).  An item is a run of "units": selected
 //   blocks (sparse) or 128-token tiles (dense).  A prologue stages the item's
 //   unit token ranges and one page id per 16-token subtile in LDS (so the
 //   streaming loop never waits on a dependent scalar load).  Waves take units
 //   round-robin and stream them one page-resident subtile at a time, keeping
-//   their own online-softmax state; the workgroup folds its four waves in LDS
+//   their own online-softmax state; the workgroup folds its eight waves in LDS
 //   and writes one (m, l, acc) partial (an empty partial when the (sequence,
 //   kv head) needs fewer items than the grid row), or the output rows directly
 //   when the grid has a single item per row.  A second small kernel merges the
@@ -131,8 +131,12 @@ struct DecodeParams {
   float* part_acc; // [batch*Hkv, max_items, G, D]
 };
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // split-K merge
 constexpr int kThreads = kWaves * 64;
+// finalize: one 8-wave workgroup per CU (two waves per SIMD), so the waves that
+// share a CU share one work list
+constexpr int kFinWaves = 8;
+constexpr int kFinThreads = kFinWaves * 64;
 constexpr int kDenseTile = 128;
 constexpr int kMaxUnitsPerItem = 512;  // LDS unit ranges per item
 constexpr int kMaxSubsPerItem = 2048;  // LDS page ids per item (16 tokens each)
@@ -248,7 +252,7 @@ __device__ __forceinline__ float mfma_row_alpha(float alpha, int i, int lane) {
 }
 
 template <int D, int G, typename KV, int SRC>
-__global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
+__global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
   constexpr int NWD = DPL * KV::kBytes / 4;
   using SM = ScoreMap<G>;
@@ -268,24 +272,26 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
   __shared__ int unit_hi[kMaxUnitsPerItem];
   __shared__ int sub_pg[kMaxSubsPerItem];    // page id of each valid subtile (kSfxPage: suffix)
   __shared__ int sub_info[kMaxSubsPerItem];  // first row in the page (or suffix token) << 5 | valid rows
-  __shared__ int wcnt_p[kWaves];
+  __shared__ int wcnt_p[kFinWaves];
+  __shared__ int wprog[kFinWaves];  // subtiles consumed per wave
   __shared__ int rc_prefix[SRC == kSrcLists ? kMaxRouteChunks + 1 : 1];
   __shared__ int rc_entries[SRC == kSrcLists ? kSpecEntries : 1];
   __shared__ float fsc[SRC == kSrcTopkFused ? kFusedMaxBlocks : 1];
   __shared__ int fsel[SRC == kSrcTopkFused ? kMaxUnitsPerItem : 1];
-  __shared__ TopkLds<kThreads> ftk;
-  __shared__ float wacc_lds[kWaves][G * D];
-  __shared__ float wm_lds[kWaves][G];
-  __shared__ float wl_lds[kWaves][G];
+  __shared__ TopkLds<kFinThreads> ftk;
+  __shared__ float wacc_lds[kFinWaves][G * D];
+  __shared__ float wm_lds[kFinWaves][G];
+  __shared__ float wl_lds[kFinWaves][G];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c16 = lane & 15;
   const int r = lane >> 4;
   const int item = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int bh = b * p.n_kv_heads + h;
+  if (threadIdx.x < kFinWaves) wprog[threadIdx.x] = 0;  // read after the prologue's barriers
 
   // ---- query rows of this kv head: raw loads issued first (independent of the
   // prologue), converted after it.  Vector path: every row at the lane's dim slice
@@ -321,14 +327,14 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
     // selects the same blocks; item 0 publishes them)
     const int nbs = min((seq_len + p.unit_tokens - 1) / p.unit_tokens, p.nb_max);
     const float* sc_row = p.scores + (int64_t)bh * p.nb_max;
-    for (int t = threadIdx.x; t < nbs; t += kThreads) fsc[t] = sc_row[t];
+    for (int t = threadIdx.x; t < nbs; t += kFinThreads) fsc[t] = sc_row[t];
     __syncthreads();
     const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
-    n_units = topk_select<kThreads>(
+    n_units = topk_select<kFinThreads>(
         ftk, [&](int j) -> u32 { return order_key(fsc[j]); }, nbs, rule, [&](int pos, int j) { fsel[pos] = j; });
     if (item == 0 && p.idx_out) {
-      for (int t = threadIdx.x; t < n_units; t += kThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
+      for (int t = threadIdx.x; t < n_units; t += kFinThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
       if (threadIdx.x == 0) p.n_sel_out[bh] = n_units;
     }
   } else if constexpr (SRC == kSrcDense) {
@@ -339,7 +345,7 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
     // counts (entries past a chunk's count are never used).
     if (p.n_rc * kRouteChunk <= kSpecEntries) {
       const int32_t* src = p.rc_lists + (int64_t)bh * p.n_rc * kRouteChunk;
-      for (int t = threadIdx.x; t < p.n_rc * kRouteChunk; t += kThreads) rc_entries[t] = src[t];
+      for (int t = threadIdx.x; t < p.n_rc * kRouteChunk; t += kFinThreads) rc_entries[t] = src[t];
     }
     if (wave == 0) {
       int run = 0;
@@ -384,7 +390,7 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
   const int nsub_u = ((SRC == kSrcLists ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
 
   // ---- prologue: token ranges of this item's units, then one page id per subtile
-  for (int t = threadIdx.x; t < nu; t += kThreads) {
+  for (int t = threadIdx.x; t < nu; t += kFinThreads) {
     const int u = u_begin + t;
     int lo = 0, hi = 0, sfx = 0;
     if constexpr (SRC == kSrcTopk || SRC == kSrcTopkFused) {
@@ -425,7 +431,7 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
   __syncthreads();
   // valid subtiles of the item in ascending order, compacted (ballots + per-wave counts)
   int n_sub = 0;  // uniform
-  for (int t0 = 0; t0 < nu * nsub_u; t0 += kThreads) {
+  for (int t0 = 0; t0 < nu * nsub_u; t0 += kFinThreads) {
     const int t = t0 + threadIdx.x;
     int pg = kNoPage, info = 0;
     if (t < nu * nsub_u) {
@@ -463,9 +469,11 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
       sub_pg[k] = pg;
       sub_info[k] = info;
     }
-    n_sub += wcnt_p[0] + wcnt_p[1] + wcnt_p[2] + wcnt_p[3];
+#pragma unroll
+    for (int w = 0; w < kFinWaves; ++w) n_sub += wcnt_p[w];
     __syncthreads();
   }
+  n_sub = __builtin_amdgcn_readfirstlane(n_sub);
 
   __syncthreads();
 
@@ -480,12 +488,13 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
     int row;  // first row within the page (suffix: first suffix token)
     int nv;   // valid rows, 1..16
   };
+  // (wave-uniform: kept in scalar registers)
   auto seek = [&](int k) -> Sub {
     if (k >= n_sub) return Sub{n_sub, 0, 0, 0};
-    const int info = sub_info[k];
-    return Sub{k, sub_pg[k], info >> 5, info & 31};
+    const int info = __builtin_amdgcn_readfirstlane(sub_info[k]);
+    return Sub{k, __builtin_amdgcn_readfirstlane(sub_pg[k]), info >> 5, info & 31};
   };
-  auto next = [&](const Sub& c) -> Sub { return seek(c.k + kWaves); };
+  auto next = [&](const Sub& c) -> Sub { return seek(c.k + kFinWaves); };
 
   // K and V row pointers of a subtile and their row strides in bytes
   auto sub_rows = [&](const Sub& sb, const char*& kp, const char*& vp, int64_t& kts, int64_t& vts) {
@@ -518,6 +527,7 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
       issue(ring[k], kbuf[k], vbuf[k]);
     }
     bool done = false;
+    int n_done = 0;
     while (!done) {
 #pragma unroll
       for (int k = 0; k < NBUF; ++k) {
@@ -530,6 +540,15 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
         ring[fk] = next(ring[pk]);
         issue(ring[fk], kbuf[fk], vbuf[fk]);
         consume(ring[k], kbuf[k], vbuf[k]);
+        // the two waves of a SIMD (w, w ^ 4) stream equal shares, but issue
+        // arbitration favours the older one; the wave ahead yields priority so
+        // both finish together (the assignment, hence the result, is unchanged)
+        ++n_done;
+        wprog[wave] = n_done;
+        const int other = wprog[wave ^ (kFinWaves / 2)];
+        if (n_done > other) __builtin_amdgcn_s_setprio(0);
+        else if (n_done < other) __builtin_amdgcn_s_setprio(2);
+        else __builtin_amdgcn_s_setprio(1);
       }
     }
   };
@@ -903,17 +922,17 @@ __global__ __launch_bounds__(kThreads, 2) void ia_condition_block_paged_finalize
   }
   __syncthreads();
 
-  // ---- fold the four waves: one (m, l, acc) per item, or the output when the item is alone
+  // ---- fold the waves: one (m, l, acc) per item, or the output when the item is alone
   const int64_t pbase = (int64_t)bh * p.max_items + item;
-  for (int o = threadIdx.x; o < G * D; o += kThreads) {
+  for (int o = threadIdx.x; o < G * D; o += kFinThreads) {
     const int g = o / D;
     float M = kNegInf;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm_lds[w][g]);
+    for (int w = 0; w < kFinWaves; ++w) M = fmaxf(M, wm_lds[w][g]);
     float a = 0.f, l = 0.f;
     if (M != kNegInf) {
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < kFinWaves; ++w) {
         const float mw = wm_lds[w][g];
         const float f = (mw == kNegInf) ? 0.f : exp2f(mw - M);
         a += f * wacc_lds[w][o];
@@ -1056,7 +1075,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
 // Per-instance launcher; returns IA_OK or an error code.
 template <int D, int G, typename KV, int SRC>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kFinThreads), 0, st, p);
   int rc = check_launch("paged decode");
   if (rc || (grid.x == 1 && !p.rep_ml)) return rc;
   hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(grid.y * grid.z), dim3(kThreads), 0, st, p,
@@ -1073,7 +1092,7 @@ int resident_wgs() {
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC>), kThreads,
+            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC>), kFinThreads,
             0) != hipSuccess)
       return 0;
     cached = std::max(1, cus * per_cu);

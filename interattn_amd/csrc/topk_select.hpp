@@ -1,14 +1,22 @@
 // Per-(sequence, kv head) top-k block selection over a row of scores held by one
 // workgroup (NT threads), shared by the standalone selector (select_topk.hip,
-// 1024 threads) and the fused top-k finalize (paged_decode_kernel.hpp, 256 threads).
+// 1024 threads) and the fused top-k finalize (paged_decode_kernel.hpp, 512 threads).
 //
 //   * forced blocks: the first forced_first and last forced_last valid blocks;
-//   * the k_eff largest remaining scores by an MSB-first 8-bit radix select on
-//     order-preserving 32-bit keys (histograms in LDS), stopping as soon as the
-//     threshold bin is taken whole; ties at the threshold go to the lowest block
-//     indices;
-//   * an ordered compaction (wave ballots + LDS offsets) emits the chosen block
-//     ids in ascending order.
+//   * the k_eff largest remaining scores, ties at the threshold going to the
+//     lowest block indices.  The selection is fixed by its last member, the
+//     threshold pair (kT, iT) in the order (score descending, index ascending):
+//     a candidate j is chosen iff key_j > kT or (key_j == kT and j <= iT), with
+//     key an order-preserving 32-bit image of the score.  The pair is found by
+//       - a 256-bucket histogram over the candidates' score range [min, max]
+//         (monotone float bucketing), whose prefix from the top names the bucket
+//         holding the threshold, then the exact rank of each of that bucket's few
+//         members (at most kTieCands of them); or, when the scores are not finite
+//         or the bucket is crowded (many equal scores),
+//       - an MSB-first 8-bit radix select on the keys (histograms in LDS),
+//         stopping as soon as the threshold bin is taken whole;
+//   * an ordered compaction (one block-wide scan of per-thread counts over
+//     contiguous index ranges) emits the chosen block ids in ascending order.
 // The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
 // with the mean key (k_bar) as the block representative.
 #pragma once
@@ -20,6 +28,10 @@ namespace ia {
 __device__ __forceinline__ u32 order_key(float s) {
   const u32 u = __float_as_uint(s);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(u32 key) {
+  return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
 }
 
 // Score of one block row held by a 16-lane row: lane c16 owns dims c16*DPL ..
@@ -43,30 +55,91 @@ __device__ __forceinline__ float block_score(const u32* w, const float* qm, floa
   return row16_sum(a) * score_scale;
 }
 
-constexpr int kTopkSubHist = 1;  // histogram copies (wave w counts into copy w % kTopkSubHist)
+constexpr int kTieCands = 128;  // threshold-bucket members ranked exactly
+constexpr int kSegElems = 16;   // most consecutive indices per thread in one scan pass
 
 template <int NT>
 struct TopkLds {
-  u32 hist[kTopkSubHist][256];
+  u32 hist[256];
   u32 red[2][NT / 64];
+  int wsum[NT / 64];
   int sh_int[4];
-  int wave_cnt[2][NT / 64];
+  u32 tie_key[kTieCands];
+  int tie_idx[kTieCands];
+  int n_tie;
+  u32 thr_key;
+  int thr_idx;
 };
 
-__device__ __forceinline__ u32 dpp_u32_max(u32 v) {
+// Maximum over the wave, all in DPP: row maxima, carried across rows by
+// row_bcast15 / row_bcast31 into lane 63, read back as a uniform value.
+__device__ __forceinline__ u32 wave_u32_max(u32 v) {
   v = max(v, (u32)__builtin_amdgcn_mov_dpp((int)v, kDppRowMirror, 0xf, 0xf, false));
   v = max(v, (u32)__builtin_amdgcn_mov_dpp((int)v, kDppRowHalfMirror, 0xf, 0xf, false));
   v = max(v, (u32)__builtin_amdgcn_mov_dpp((int)v, kDppXor2, 0xf, 0xf, false));
   v = max(v, (u32)__builtin_amdgcn_mov_dpp((int)v, kDppXor1, 0xf, 0xf, false));
-  v = max(v, (u32)__shfl_xor((int)v, 16, 64));
-  return max(v, (u32)__shfl_xor((int)v, 32, 64));
+  v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast15, 0xa, 0xf, false));
+  v = max(v, (u32)__builtin_amdgcn_update_dpp(0, (int)v, kDppRowBcast31, 0xc, 0xf, false));
+  return (u32)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Exclusive prefix sum of one int per thread over the workgroup (thread order);
+// *total receives the sum.  Every thread calls it; two barriers.
+template <int NT>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* wsum, int* total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int inc = wave_inclusive_scan(v);
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    const int s = wsum[w];
+    tot += s;
+    before += (w < wave) ? s : 0;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + inc - v;
+}
+
+// Wave 0 of the workgroup: the histogram bin (scanned from the top) where the
+// running count first reaches `remaining`; writes sh_int[1..3] = (bin, count still
+// needed inside it, members of it).  The caller synchronises.
+template <int NT>
+__device__ __forceinline__ void threshold_bin(TopkLds<NT>& L, int remaining) {
+  const int lane = threadIdx.x & 63;
+  // bins in descending order: lane l owns bins 255-4l .. 252-4l
+  u32 c[4];
+  u32 tot = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    c[t] = L.hist[255 - 4 * lane - t];
+    tot += c[t];
+  }
+  const u32 inc = (u32)wave_inclusive_scan((int)tot);  // over lanes, descending-bin order
+  const u32 exc = inc - tot;
+  if (exc < (u32)remaining && inc >= (u32)remaining) {
+    u32 run = exc;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (run + c[t] >= (u32)remaining) {
+        L.sh_int[1] = 255 - 4 * lane - t;
+        L.sh_int[2] = remaining - (int)run;
+        L.sh_int[3] = (int)c[t];
+        break;
+      }
+      run += c[t];
+    }
+  }
 }
 
 struct TopkRule {
   int forced_first, forced_last, k, forced_in_k, k_cap;
 };
 
-// Every thread of the workgroup calls this (it synchronises).  key_at(j) returns
+// Every thread of the workgroup calls this (it synchronises, also on return).  key_at(j) returns
 // order_key(score_j) for 0 <= j < nb; emit(pos, j) is called for each chosen block,
 // pos = 0, 1, ... in ascending block order (only pos < k_cap).  Returns the number
 // of chosen blocks (clamped to k_cap).
@@ -83,14 +156,18 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
   int k_eff = rule.forced_in_k ? rule.k - n_forced : rule.k;
   k_eff = max(k_eff, 0);
   k_eff = min(k_eff, max(rule.k_cap - n_forced, 0));
+  // consecutive indices per thread in the scans over the row (all threads busy)
+  const int seg = min(kSegElems, max(1, (nb + NT - 1) / NT));
 
-  u32 thr = 0u;       // threshold prefix; candidates with (key & thr_mask) > thr are taken
-  u32 thr_mask = 0u;
-  int take_ties = 0;  // candidates with (key & thr_mask) == thr taken, lowest indices first
-  const bool take_all = k_eff >= n_cand;
-  if (!take_all && k_eff > 0) {
-    // the candidates' largest and smallest keys: the bytes they share are common to
-    // every candidate, so the radix passes start at the first byte that differs
+  // threshold pair: every candidate when all are taken, none when k_eff == 0
+  u32 kT = 0u;
+  int iT = 0x7fffffff;
+  if (k_eff == 0) {
+    kT = 0xffffffffu;
+    iT = -1;
+  }
+  if (k_eff > 0 && k_eff < n_cand) {
+    // ---- the candidates' largest and smallest keys
     u32 kmx = 0u, kmn_inv = 0u;  // max key, max of ~key
     for (int j = threadIdx.x; j < nb; j += NT) {
       if (is_forced(j)) continue;
@@ -98,127 +175,160 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
       kmx = max(kmx, key);
       kmn_inv = max(kmn_inv, ~key);
     }
-    kmx = dpp_u32_max(kmx);
-    kmn_inv = dpp_u32_max(kmn_inv);
+    kmx = wave_u32_max(kmx);
+    kmn_inv = wave_u32_max(kmn_inv);
     if (lane == 0) {
       L.red[0][wave] = kmx;
       L.red[1][wave] = kmn_inv;
     }
+    for (int t = threadIdx.x; t < 256; t += NT) L.hist[t] = 0u;
+    if (threadIdx.x == 0) L.n_tie = 0;
     __syncthreads();
     kmx = 0u;
     kmn_inv = 0u;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) {
+    for (int w = 0; w < kWv; ++w) {
       kmx = max(kmx, L.red[0][w]);
       kmn_inv = max(kmn_inv, L.red[1][w]);
     }
-    const u32 diff = kmx ^ ~kmn_inv;
-    const int common_bytes = diff == 0u ? 4 : (__clz((int)diff) >> 3);
-    u32 prefix = 0u, mask = 0u;
-    if (common_bytes > 0) {
-      mask = common_bytes == 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * common_bytes));
-      prefix = kmx & mask;
-    }
-    int remaining = k_eff;
-    for (int shift = 24 - 8 * common_bytes; shift >= 0; shift -= 8) {
-      for (int t = threadIdx.x; t < kTopkSubHist * 256; t += NT) (&L.hist[0][0])[t] = 0u;
-      __syncthreads();
-      u32* hist = L.hist[wave % kTopkSubHist];
+    const u32 kmn = ~kmn_inv;
+
+    // ---- fast path: buckets over the finite score range, exact ranks in the
+    // threshold bucket (the decision is uniform over the workgroup)
+    const float fmax = key_value(kmx), fmin = key_value(kmn);
+    const float bscale = 256.f / (fmax - fmin);
+    bool fast = __builtin_isfinite(fmax) && __builtin_isfinite(fmin) && __builtin_isfinite(bscale) && bscale > 0.f;
+    auto bucket = [&](u32 key) { return min(255, (int)((key_value(key) - fmin) * bscale)); };
+    if (fast) {
       for (int j = threadIdx.x; j < nb; j += NT) {
         if (is_forced(j)) continue;
-        const u32 key = key_at(j);
-        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        atomicAdd(&L.hist[bucket(key_at(j))], 1u);
       }
       __syncthreads();
-      if (wave == 0) {
-        // bins in descending order: lane l owns bins 255-4l .. 252-4l
-        u32 c[4];
-        u32 tot = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          c[t] = 0u;
-#pragma unroll
-          for (int h = 0; h < kTopkSubHist; ++h) c[t] += L.hist[h][255 - 4 * lane - t];
-          tot += c[t];
-        }
-        u32 inc = tot;  // inclusive scan over lanes (descending-bin order)
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const u32 o = __shfl_up(inc, off, 64);
-          if (lane >= off) inc += o;
-        }
-        const u32 exc = inc - tot;
-        // the bin where the running count first reaches `remaining`
-        if (exc < (u32)remaining && inc >= (u32)remaining) {
-          u32 run = exc;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            if (run + c[t] >= (u32)remaining) {
-              L.sh_int[1] = 255 - 4 * lane - t;    // digit
-              L.sh_int[2] = remaining - (int)run;  // still needed inside this bin
-              L.sh_int[3] = (int)c[t];             // candidates inside this bin
-              break;
-            }
-            run += c[t];
+      if (wave == 0) threshold_bin<NT>(L, k_eff);
+      __syncthreads();
+      const int tb = L.sh_int[1];
+      const int need = L.sh_int[2];
+      const int in_bin = L.sh_int[3];
+      if (in_bin <= kTieCands) {
+        for (int j = threadIdx.x; j < nb; j += NT) {
+          if (is_forced(j)) continue;
+          const u32 key = key_at(j);
+          if (bucket(key) == tb) {
+            const int s = atomicAdd(&L.n_tie, 1);
+            L.tie_key[s] = key;
+            L.tie_idx[s] = j;
           }
         }
+        __syncthreads();
+        // member i's rank among the bucket's members; rank need - 1 is the threshold
+        for (int i = threadIdx.x; i < in_bin; i += NT) {
+          const u32 ki = L.tie_key[i];
+          const int ji = L.tie_idx[i];
+          int rank = 0;
+          for (int e = 0; e < in_bin; ++e) {
+            const u32 ke = L.tie_key[e];
+            rank += (ke > ki || (ke == ki && L.tie_idx[e] < ji)) ? 1 : 0;
+          }
+          if (rank == need - 1) {
+            L.thr_key = ki;
+            L.thr_idx = ji;
+          }
+        }
+        __syncthreads();
+        kT = L.thr_key;
+        iT = L.thr_idx;
+      } else {
+        fast = false;
       }
-      __syncthreads();
-      const u32 digit = (u32)L.sh_int[1];
-      remaining = L.sh_int[2];
-      const int in_bin = L.sh_int[3];
-      prefix |= digit << shift;
-      mask |= 255u << shift;
-      __syncthreads();
-      if (remaining == in_bin) break;  // the whole bin is taken: the threshold is exact
     }
-    thr = prefix;
-    thr_mask = mask;
-    take_ties = remaining;
+
+    if (!fast) {
+      // ---- radix select on the keys: the bytes every candidate shares are skipped
+      const u32 diff = kmx ^ kmn;
+      const int common_bytes = diff == 0u ? 4 : (__clz((int)diff) >> 3);
+      u32 prefix = 0u, mask = 0u;
+      if (common_bytes > 0) {
+        mask = common_bytes == 4 ? 0xffffffffu : ~(0xffffffffu >> (8 * common_bytes));
+        prefix = kmx & mask;
+      }
+      int remaining = k_eff;
+      int in_bin = n_cand;
+      for (int shift = 24 - 8 * common_bytes; shift >= 0; shift -= 8) {
+        for (int t = threadIdx.x; t < 256; t += NT) L.hist[t] = 0u;
+        __syncthreads();
+        for (int j = threadIdx.x; j < nb; j += NT) {
+          if (is_forced(j)) continue;
+          const u32 key = key_at(j);
+          if ((key & mask) == prefix) atomicAdd(&L.hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (wave == 0) threshold_bin<NT>(L, remaining);
+        __syncthreads();
+        const u32 digit = (u32)L.sh_int[1];
+        remaining = L.sh_int[2];
+        in_bin = L.sh_int[3];
+        prefix |= digit << shift;
+        mask |= 255u << shift;
+        __syncthreads();
+        if (remaining == in_bin) break;  // the whole bin is taken: the threshold is exact
+      }
+      kT = prefix;  // keys with (key & mask) >= prefix, i.e. key >= prefix (low bits zero)
+      if (remaining != in_bin) {
+        // mask is full: take the `remaining` lowest indices among keys equal to prefix
+        int base = 0;
+        for (int c0 = 0; c0 < nb; c0 += NT * seg) {
+          const int j0 = c0 + threadIdx.x * seg;
+          int cnt = 0;
+          for (int e = 0; e < seg; ++e) {
+            const int j = j0 + e;
+            cnt += (j < nb && !is_forced(j) && key_at(j) == prefix) ? 1 : 0;
+          }
+          int total;
+          const int before = base + block_exclusive_scan<NT>(cnt, L.wsum, &total);
+          if (before < remaining && before + cnt >= remaining) {
+            int run = before;
+            for (int e = 0; e < seg; ++e) {
+              const int j = j0 + e;
+              if (j < nb && !is_forced(j) && key_at(j) == prefix && ++run == remaining) L.thr_idx = j;
+            }
+          }
+          base += total;
+          if (base >= remaining) break;  // uniform
+        }
+        __syncthreads();
+        iT = L.thr_idx;
+      }
+    }
   }
 
-  // ordered compaction
-  int base_sel = 0, base_tie = 0;
-  for (int j0c = 0; j0c < nb; j0c += NT) {
-    const int j = j0c + threadIdx.x;
-    bool forced = false, above = false, tie = false;
-    if (j < nb) {
-      forced = is_forced(j);
-      if (!forced) {
-        if (take_all) {
-          above = true;
-        } else if (k_eff > 0) {
-          const u32 key = key_at(j) & thr_mask;
-          above = key > thr;
-          tie = key == thr;
+  // ---- ordered compaction: each thread scans `seg` consecutive indices
+  int base_sel = 0;
+  for (int c0 = 0; c0 < nb; c0 += NT * seg) {
+    const int j0 = c0 + threadIdx.x * seg;
+    u32 bits = 0u;
+    for (int e = 0; e < seg; ++e) {
+      const int j = j0 + e;
+      if (j < nb) {
+        bool sel = is_forced(j);
+        if (!sel) {
+          const u32 key = key_at(j);
+          sel = key > kT || (key == kT && j <= iT);
         }
+        bits |= sel ? (1u << e) : 0u;
       }
     }
-    // tie rank in index order
-    const unsigned long long tb = __ballot(tie);
-    const int tie_rank_in_wave = __popcll(tb & ((1ull << lane) - 1ull));
-    if (lane == 0) L.wave_cnt[1][wave] = __popcll(tb);
-    __syncthreads();
-    int tie_off = base_tie;
-    for (int w = 0; w < wave; ++w) tie_off += L.wave_cnt[1][w];
-    const bool take_tie = tie && (tie_off + tie_rank_in_wave < take_ties);
-    const bool sel = forced || above || take_tie;
-    const unsigned long long sb = __ballot(sel);
-    const int sel_rank = __popcll(sb & ((1ull << lane) - 1ull));
-    if (lane == 0) L.wave_cnt[0][wave] = __popcll(sb);
-    __syncthreads();
-    int sel_off = base_sel;
-    for (int w = 0; w < wave; ++w) sel_off += L.wave_cnt[0][w];
-    if (sel && sel_off + sel_rank < rule.k_cap) emit(sel_off + sel_rank, j);
-    int tot_s = 0, tot_t = 0;
-    for (int w = 0; w < kWv; ++w) {
-      tot_s += L.wave_cnt[0][w];
-      tot_t += L.wave_cnt[1][w];
+    int total;
+    int pos = base_sel + block_exclusive_scan<NT>(__popc(bits), L.wsum, &total);
+    while (bits) {
+      const int e = __ffs((int)bits) - 1;
+      bits &= bits - 1u;
+      if (pos < rule.k_cap) emit(pos, j0 + e);
+      ++pos;
     }
-    base_sel += tot_s;
-    base_tie += tot_t;
-    __syncthreads();
+    base_sel += total;
   }
+  __syncthreads();  // emitted entries (e.g. in LDS) are visible to the workgroup on return
   return min(base_sel, rule.k_cap);
 }
 

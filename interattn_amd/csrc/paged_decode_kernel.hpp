@@ -327,11 +327,23 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     // selects the same blocks; item 0 publishes them)
     const int nbs = min((seq_len + p.unit_tokens - 1) / p.unit_tokens, p.nb_max);
     const float* sc_row = p.scores + (int64_t)bh * p.nb_max;
-    for (int t = threadIdx.x; t < nbs; t += kFinThreads) fsc[t] = sc_row[t];
-    __syncthreads();
     const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
-    n_units = topk_select<kFinThreads>(
+    // staging the row also gives the selection its candidates' key range
+    const TopkForced forced(rule, nbs);
+    u32 kmx = 0u, kmn_inv = 0u;
+    for (int t = threadIdx.x; t < nbs; t += kFinThreads) {
+      const float v = sc_row[t];
+      fsc[t] = v;
+      if (!forced(t)) {
+        const u32 key = order_key(v);
+        kmx = max(kmx, key);
+        kmn_inv = max(kmn_inv, ~key);
+      }
+    }
+    topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
+    __syncthreads();
+    n_units = topk_select<kFinThreads, true>(
         ftk, [&](int j) -> u32 { return order_key(fsc[j]); }, nbs, rule, [&](int pos, int j) { fsel[pos] = j; });
     if (item == 0 && p.idx_out) {
       for (int t = threadIdx.x; t < n_units; t += kFinThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
@@ -952,12 +964,14 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
 }
 
 constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
+constexpr int kMergeFastSlots = 8;  // up to this many slots: one round trip, one wave
 
 // Split-K merge, one workgroup per (sequence, kv head): out = sum_s f_s acc_s / sum_s f_s l_s
 // with f_s = 2^(m_s - M) over the finalize items' partials and the route chunks'
-// representative partials (CBT/legacy.py:765-794).  Two dependent global round
-// trips: every slot's (m, l) is staged in LDS at once, then the accumulators of
-// the non-empty slots are read with many loads in flight.
+// representative partials (CBT/legacy.py:765-794).  Up to kMergeFastSlots slots
+// one wave reads every (m, l) and accumulator in one round trip.  Beyond that, two
+// dependent round trips: every slot's (m, l) is staged in LDS at once, then the
+// accumulators of the non-empty slots are read with many loads in flight.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
   __shared__ float m_lds[kMaxMergeSlots][G];
@@ -980,6 +994,53 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
     return s < n_slots ? p.part_acc + ((int64_t)bh * p.max_items + s) * (G * D)
                        : p.rep_acc + ((int64_t)bh * p.n_rc + (s - n_slots)) * (G * D);
   };
+  constexpr int PER = G * D / 64;  // outputs per lane of one wave (all in query row o0 / D)
+  if (n_all <= kMergeFastSlots) {
+    // few slots: wave 0 loads every slot's (m, l) and accumulators in one round trip
+    if (wave != 0) return;
+    const int o0 = lane * PER;
+    const int g0 = o0 / D;
+    float mv[kMergeFastSlots], lv[kMergeFastSlots], av[kMergeFastSlots][PER];
+#pragma unroll
+    for (int s = 0; s < kMergeFastSlots; ++s) {
+      mv[s] = kNegInf;
+      lv[s] = 0.f;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
+      if (s < n_all) {
+        const float* ml = ml_of(s) + g0 * 2;
+        mv[s] = ml[0];
+        lv[s] = ml[1];
+        const float* src = acc_of(s) + o0;
+        if constexpr (PER % 4 == 0) {
+#pragma unroll
+          for (int e = 0; e < PER; e += 4) {
+            const float4 w4 = *reinterpret_cast<const float4*>(src + e);
+            av[s][e] = w4.x; av[s][e + 1] = w4.y; av[s][e + 2] = w4.z; av[s][e + 3] = w4.w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < PER; ++e) av[s][e] = src[e];
+        }
+      }
+    }
+    float M = kNegInf;
+#pragma unroll
+    for (int s = 0; s < kMergeFastSlots; ++s) M = fmaxf(M, mv[s]);
+    float L = 0.f, a[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) a[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMergeFastSlots; ++s) {
+      const float f = (mv[s] == kNegInf) ? 0.f : exp2f(mv[s] - M);
+      L += f * lv[s];
+#pragma unroll
+      for (int e = 0; e < PER; ++e) a[e] = fmaf(f, av[s][e], a[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) store_decode_out<G, D>(p, b, h, o0 + e, a[e] / fmaxf(L, 1e-30f));
+    return;
+  }
   for (int t = threadIdx.x; t < n_all * G; t += kThreads) {
     const int s = t / G, g = t - s * G;
     const float* ml = ml_of(s) + g * 2;
@@ -1023,7 +1084,6 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   __syncthreads();
   // accumulators: wave w folds list entries w, w + 4, ...; lane owns PER consecutive
   // outputs of the slot's [G, D] block (vector loads), kU slots in flight
-  constexpr int PER = G * D / 64;
   constexpr int kU = 4;
   const int nl = n_list;
   const int o0 = lane * PER;

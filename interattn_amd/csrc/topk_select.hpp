@@ -139,18 +139,43 @@ struct TopkRule {
   int forced_first, forced_last, k, forced_in_k, k_cap;
 };
 
+// Blocks [0, ff) and [fl_start, nb) are forced in; the others are candidates.
+struct TopkForced {
+  int ff, fl_start;
+  __device__ TopkForced(const TopkRule& rule, int nb)
+      : ff(min(max(rule.forced_first, 0), nb)), fl_start(max(nb - max(rule.forced_last, 0), 0)) {}
+  __device__ bool operator()(int j) const { return j < ff || j >= fl_start; }
+};
+
+// Staged start of topk_select (for a caller that already walks the score row, e.g.
+// while copying it to LDS): each thread passes the largest key and the largest ~key
+// of the candidates it saw; the per-wave values land in L.red and the histogram is
+// cleared.  The caller synchronises the workgroup before topk_select<..., staged>.
+template <int NT>
+__device__ __forceinline__ void topk_stage(TopkLds<NT>& L, u32 kmx, u32 kmn_inv) {
+  const int wave = threadIdx.x >> 6;
+  kmx = wave_u32_max(kmx);
+  kmn_inv = wave_u32_max(kmn_inv);
+  if ((threadIdx.x & 63) == 0) {
+    L.red[0][wave] = kmx;
+    L.red[1][wave] = kmn_inv;
+  }
+  for (int t = threadIdx.x; t < 256; t += NT) L.hist[t] = 0u;
+  if (threadIdx.x == 0) L.n_tie = 0;
+}
+
 // Every thread of the workgroup calls this (it synchronises, also on return).  key_at(j) returns
 // order_key(score_j) for 0 <= j < nb; emit(pos, j) is called for each chosen block,
 // pos = 0, 1, ... in ascending block order (only pos < k_cap).  Returns the number
-// of chosen blocks (clamped to k_cap).
-template <int NT, typename KeyAt, typename Emit>
+// of chosen blocks (clamped to k_cap).  STAGED: the caller ran topk_stage and a
+// workgroup barrier (the first pass over the row is skipped).
+template <int NT, bool STAGED = false, typename KeyAt, typename Emit>
 __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule& rule, Emit emit) {
   constexpr int kWv = NT / 64;
-  const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int ff = min(max(rule.forced_first, 0), nb);
-  const int fl_start = max(nb - max(rule.forced_last, 0), 0);
-  auto is_forced = [&](int j) { return j < ff || j >= fl_start; };
+  const TopkForced is_forced(rule, nb);
+  const int ff = is_forced.ff;
+  const int fl_start = is_forced.fl_start;
   const int n_forced = ff + (nb - max(fl_start, ff));  // |[0,ff) U [fl_start,nb)|
   const int n_cand = nb - n_forced;
   int k_eff = rule.forced_in_k ? rule.k - n_forced : rule.k;
@@ -169,23 +194,18 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
   if (k_eff > 0 && k_eff < n_cand) {
     // ---- the candidates' largest and smallest keys
     u32 kmx = 0u, kmn_inv = 0u;  // max key, max of ~key
-    for (int j = threadIdx.x; j < nb; j += NT) {
-      if (is_forced(j)) continue;
-      const u32 key = key_at(j);
-      kmx = max(kmx, key);
-      kmn_inv = max(kmn_inv, ~key);
+    if constexpr (!STAGED) {
+      for (int j = threadIdx.x; j < nb; j += NT) {
+        if (is_forced(j)) continue;
+        const u32 key = key_at(j);
+        kmx = max(kmx, key);
+        kmn_inv = max(kmn_inv, ~key);
+      }
+      topk_stage<NT>(L, kmx, kmn_inv);
+      __syncthreads();
+      kmx = 0u;
+      kmn_inv = 0u;
     }
-    kmx = wave_u32_max(kmx);
-    kmn_inv = wave_u32_max(kmn_inv);
-    if (lane == 0) {
-      L.red[0][wave] = kmx;
-      L.red[1][wave] = kmn_inv;
-    }
-    for (int t = threadIdx.x; t < 256; t += NT) L.hist[t] = 0u;
-    if (threadIdx.x == 0) L.n_tie = 0;
-    __syncthreads();
-    kmx = 0u;
-    kmn_inv = 0u;
 #pragma unroll
     for (int w = 0; w < kWv; ++w) {
       kmx = max(kmx, L.red[0][w]);

@@ -275,10 +275,8 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
   // chunk partials over the 16 blocks: 4 steps in-lane, 4 rows across lanes
   float mz = fmaxf(fmaxf(zs[0], zs[1]), fmaxf(zs[2], zs[3]));
   float mc = fmaxf(fmaxf(zcs[0], zcs[1]), fmaxf(zcs[2], zcs[3]));
-  mz = fmaxf(mz, shfl_xor_f(mz, 16));
-  mz = fmaxf(mz, shfl_xor_f(mz, 32));
-  mc = fmaxf(mc, shfl_xor_f(mc, 16));
-  mc = fmaxf(mc, shfl_xor_f(mc, 32));
+  mz = rows_max(mz);
+  mc = rows_max(mc);
   float lz = 0.f, lc = 0.f;
   if (mz != kNegInf) {
 #pragma unroll
@@ -288,10 +286,8 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
 #pragma unroll
     for (int t = 0; t < 4; ++t) lc += (zcs[t] == kNegInf) ? 0.f : __expf(zcs[t] - mc);
   }
-  lz += shfl_xor_f(lz, 16);
-  lz += shfl_xor_f(lz, 32);
-  lc += shfl_xor_f(lc, 16);
-  lc += shfl_xor_f(lc, 32);
+  lz = rows_sum(lz);
+  lc = rows_sum(lc);
   if (r == 0 && c16 < G) {
     const int rows = p.n_kv_heads * G;
     const int64_t base = (int64_t)b * 4 * rows * p.n_chunks + (int64_t)(h * G + c16) * p.n_chunks + chunk;
@@ -518,9 +514,7 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   float mg[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float m = z_lds[g][threadIdx.x];
-#pragma unroll
-    for (int o2 = 32; o2 >= 1; o2 >>= 1) m = fmaxf(m, __shfl_xor(m, o2, 64));
+    const float m = wave_max(z_lds[g][threadIdx.x]);
     if (lane == 0) red[wave][g] = m;
   }
   __syncthreads();
@@ -532,9 +526,7 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
     const float zv = z_lds[g][threadIdx.x];
     const float beta = (zv == kNegInf) ? 0.f : __expf(zv - mg[g]);
     z_lds[g][threadIdx.x] = beta;  // reuse as the fp32 weight
-    float l = beta;
-#pragma unroll
-    for (int o2 = 32; o2 >= 1; o2 >>= 1) l += __shfl_xor(l, o2, 64);
+    const float l = wave_sum(beta);
     if (lane == 0) red[4 + wave][g] = l;
   }
   __syncthreads();
@@ -559,8 +551,7 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
       float v = acc[g][e];
-      v += shfl_xor_f(v, 16);
-      v += shfl_xor_f(v, 32);
+      v = rows_sum(v);
       if (r == 0) wacc[wave][g * D + c16 * DPL + e] = v;
     }
   __syncthreads();

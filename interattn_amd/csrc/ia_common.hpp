@@ -100,6 +100,23 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
   return v;
 }
 
+// Maximum / sum over the four 16-lane rows (lanes c, c+16, c+32, c+48), every lane
+// receiving the result, on the VALU (gfx950 permlane swaps; no LDS crossbar):
+// swapping a register with itself leaves lane l the pair {v[l], v[l ^ 32]}, then
+// {v[l], v[l ^ 16]}.
+__device__ __forceinline__ float rows_max(float v) {
+  auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+  t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+  t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
 // Sum over the 16 lanes of a row; every lane receives the total.  Partner sets
 // of mirror, half-mirror, xor2, xor1 are disjoint at each step.
 __device__ __forceinline__ float row16_sum(float v) {
@@ -154,16 +171,8 @@ __device__ __forceinline__ float row16_max(float v) {
 }
 
 // Reductions over the 64 lanes of a wave; every lane receives the result.
-__device__ __forceinline__ float wave_sum(float v) {
-  v = row16_sum(v);
-  v += shfl_xor_f(v, 16);
-  return v + shfl_xor_f(v, 32);
-}
-__device__ __forceinline__ float wave_max(float v) {
-  v = row16_max(v);
-  v = fmaxf(v, shfl_xor_f(v, 16));
-  return fmaxf(v, shfl_xor_f(v, 32));
-}
+__device__ __forceinline__ float wave_sum(float v) { return rows_sum(row16_sum(v)); }
+__device__ __forceinline__ float wave_max(float v) { return rows_max(row16_max(v)); }
 
 // Wave-level barrier for LDS traffic that stays inside one wavefront.
 __device__ __forceinline__ void wave_lds_sync() {

@@ -164,9 +164,7 @@ __device__ __forceinline__ float fold_g(float v) {
   v = op(v, dpp<kDppRowRor8>(v));
   if constexpr (G <= 2) v = op(v, dpp<kDppXor1>(v));
   if constexpr (G == 1) v = op(v, dpp<kDppXor2>(v));
-  v = op(v, shfl_xor_f(v, 16));
-  v = op(v, shfl_xor_f(v, 32));
-  return v;
+  return MAX ? rows_max(v) : rows_sum(v);
 }
 
 template <int G, int D>
@@ -642,7 +640,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         }
       }
       // ---------------- online softmax, one update per subtile (max over the 16
-      // tokens: in-lane over i, then over the four lane rows)
+      // tokens: in-lane over i, then over the four lane rows with permlane swaps)
       float sv[4];
       float mt = kNegInf;
 #pragma unroll
@@ -650,8 +648,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         sv[i] = (r + 4 * i < sb.nv) ? s[i] * sc : kNegInf;
         mt = fmaxf(mt, sv[i]);
       }
-      mt = fmaxf(mt, shfl_xor_f(mt, 16));
-      mt = fmaxf(mt, shfl_xor_f(mt, 32));
+      mt = rows_max(mt);
       const float m_new = fmaxf(m_run, mt);
       float pw[4];
 #pragma unroll
@@ -700,8 +697,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
 
     // ---- fold the wave: l over the four lane rows; the query rows' accumulators sit
     // in lane rows r < max(1, G/4) (row 4r + i < G)
-    l_run += shfl_xor_f(l_run, 16);
-    l_run += shfl_xor_f(l_run, 32);
+    l_run = rows_sum(l_run);
     if (r == 0 && c16 < G) {
       wm_lds[wave][c16] = m_run;
       wl_lds[wave][c16] = l_run;
@@ -1052,8 +1048,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   for (int g = wave; g < G; g += kWaves) {
     float M = kNegInf;
     for (int s = lane; s < n_all; s += 64) M = fmaxf(M, m_lds[s][g]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    M = wave_max(M);
     float L = 0.f;
     for (int s = lane; s < n_all; s += 64) {
       const float m = m_lds[s][g];
@@ -1061,8 +1056,7 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
       m_lds[s][g] = f;
       L += f * l_lds[s][g];
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) L += __shfl_xor(L, off, 64);
+    L = wave_sum(L);
     if (lane == 0) lsum[g] = L;
   }
   __syncthreads();

@@ -170,6 +170,17 @@ IA_API int ia_select_topk(const ia_decode_shape* shape, const void* q, const voi
                    size_t workspace_bytes, void* stream);
 
 /*
+ * Block mask [batch, n_kv_heads, nb] uint8 of a top-k selection: 1 for the blocks
+ * idx[b, h, 0:n_sel[b, h]] (ids outside [0, nb) ignored), 0 elsewhere.  With
+ * ia_fixed_mask_decode it gives the top-k finalize with representatives for the
+ * unselected blocks (the external-mask semantics of fixed_mask_hybrid_attention,
+ * CBG/real_attention_benchmark/fixed_mask.py:38-239, applied to a top-k
+ * selection); no single reference function corresponds.
+ */
+IA_API int ia_topk_block_mask(const int32_t* idx, const int32_t* n_sel, int32_t k_cap, int32_t batch,
+                              int32_t n_kv_heads, int32_t nb, uint8_t* mask, void* stream);
+
+/*
  * Sparse paged decode (finalize attention over selected blocks).  For each
  * (b, q row) the softmax of q . K^T * scale over the valid tokens of the blocks
  * idx[b, h, 0:n_sel[b,h]] (block_size tokens each), applied to V; split-K over

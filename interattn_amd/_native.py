@@ -155,6 +155,7 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _P, ctypes.POINTER(PagedKV),
          ctypes.POINTER(SuffixKV), _F, _P, _I32, _P, _SZ, _P]),
+    "ia_topk_block_mask": (ctypes.c_int, [_P, _P, _I32, _I32, _I32, _I32, _P, _P]),
     "ia_sparse_max_items": (_I32, [_I32, _I32, _I32]),
     "ia_dense_max_items": (_I32, [_I32, _I32, _I32]),
 }

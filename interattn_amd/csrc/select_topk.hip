@@ -272,7 +272,39 @@ int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_b
 
 }  // namespace ia
 
+namespace ia {
+
+// Block mask [batch, Hkv, nb] of a top-k selection: one workgroup per (sequence, kv
+// head) clears its row, then marks blocks idx[b, h, 0:n_sel] (ids outside [0, nb)
+// are ignored).  Consumed by the fixed-mask hybrid decode (representatives for the
+// unselected blocks).
+__global__ __launch_bounds__(256) void ia_topk_block_mask_kernel(const int32_t* idx, const int32_t* n_sel,
+                                                                 int32_t k_cap, int32_t nb, uint8_t* mask) {
+  const int bh = blockIdx.y * gridDim.x + blockIdx.x;
+  uint8_t* row = mask + (int64_t)bh * nb;
+  for (int j = threadIdx.x; j < nb; j += 256) row[j] = 0;
+  __syncthreads();
+  const int n = min(max(n_sel[bh], 0), k_cap);
+  for (int t = threadIdx.x; t < n; t += 256) {
+    const int j = idx[(int64_t)bh * k_cap + t];
+    if (j >= 0 && j < nb) row[j] = 1;
+  }
+}
+
+}  // namespace ia
+
 extern "C" {
+
+int ia_topk_block_mask(const int32_t* idx, const int32_t* n_sel, int32_t k_cap, int32_t batch, int32_t n_kv_heads,
+                       int32_t nb, uint8_t* mask, void* stream) {
+  using namespace ia;
+  if (batch < 0 || n_kv_heads <= 0 || nb < 0 || k_cap <= 0) return fail(IA_ERR_INVALID, "bad mask shape");
+  if (batch == 0 || nb == 0) return IA_OK;
+  if (!idx || !n_sel || !mask) return fail(IA_ERR_INVALID, "idx, n_sel and mask must be non-null");
+  hipLaunchKernelGGL(ia_topk_block_mask_kernel, dim3(n_kv_heads, batch), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), idx, n_sel, k_cap, nb, mask);
+  return check_launch("top-k block mask");
+}
 
 size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t nb_max) {
   return ia::select_ws_size(batch, n_kv_heads, nb_max);

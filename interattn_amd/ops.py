@@ -294,11 +294,25 @@ def _out_tensor(q, out, out_dtype, workspace):
 
 
 def sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, *, block_size, scale=None,
-                        scales=None, out=None, out_dtype=None, workspace=None):
+                        scales=None, include_representatives=False, summaries=None, out=None, out_dtype=None,
+                        workspace=None):
     """Attention over the selected blocks only: for each query row, softmax(q.K^T*scale)
     over the valid tokens of blocks ``idx[b, h, :n_sel[b, h]]``, applied to V.  The
     top-k form of the finalize stage (CBT/page_attention.py:206-255 + the split-K merge
-    of CBT/legacy.py:765-794).  Returns ``[B, Hq, D]`` (``out`` when given)."""
+    of CBT/legacy.py:765-794).  Returns ``[B, Hq, D]`` (``out`` when given).
+
+    ``include_representatives=True`` adds one representative per unselected non-empty
+    block in the same softmax: logit ``q.k_bar/sqrt(D) + log(count)`` (q, k_bar rounded
+    to bf16 for bf16 caches) and value ``v_bar``, the external-mask semantics of
+    fixed_mask_hybrid_attention (CBG/real_attention_benchmark/fixed_mask.py:38-239).
+    It needs ``summaries`` from ``build_block_summaries(..., full=True)`` at the same
+    ``block_size`` (valid tokens per block are the summaries' counts) and bf16 or fp32
+    K/V."""
+    if include_representatives:
+        return _sparse_decode_with_representatives(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel,
+                                                   block_size=block_size, scale=scale, scales=scales,
+                                                   summaries=summaries, out=out, out_dtype=out_dtype,
+                                                   workspace=workspace)
     kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
     _require_cuda(q, seq_lens, idx, n_sel)
     hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
@@ -326,6 +340,77 @@ def sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, *,
     rc = lib.ia_sparse_paged_decode(
         sh, q.data_ptr(), kv, seq_lens.data_ptr(), int(block_size), idx.data_ptr(), k_cap, n_sel.data_ptr(),
         scale, out.data_ptr(), _code(out.dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
+    N.check(rc)
+    del keep
+    return out
+
+
+def _paged_summaries_desc(summaries, b, hkv, d, block_size):
+    """C-ABI view of ``build_block_summaries(..., full=True)`` output ([B, Hkv, nb, D])."""
+    if summaries is None:
+        raise ValueError("include_representatives needs summaries=build_block_summaries(..., full=True)")
+    need = ("k_bar", "v_bar", "block_valid_counts", "v_norm_max", "v_norm_all")
+    miss = [k for k in need if summaries.get(k) is None]
+    if miss:
+        raise ValueError(f"summaries lack {miss}: build them with full=True")
+    k_bar, v_bar = summaries["k_bar"], summaries["v_bar"]
+    nb = int(k_bar.shape[2]) if k_bar.dim() == 4 else -1
+    for name in ("k_bar", "v_bar"):
+        t = summaries[name]
+        if t.dim() != 4 or tuple(t.shape) != (b, hkv, nb, d) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [B, Hkv, nb, D] tensor")
+    _check_i32(summaries["block_valid_counts"], "block_valid_counts", (b, nb))
+    vnm, vna = summaries["v_norm_max"], summaries["v_norm_all"]
+    if vnm.dtype != torch.float32 or vna.dtype != torch.float32 or not vnm.is_contiguous():
+        raise ValueError("v_norm_max and v_norm_all must be contiguous float32")
+    sm = N.BlockSummaries()
+    sm.k_bar, sm.v_bar = k_bar.data_ptr(), v_bar.data_ptr()
+    sm.k_max = summaries["k_max"].data_ptr() if summaries.get("k_max") is not None else None
+    sm.k_min = summaries["k_min"].data_ptr() if summaries.get("k_min") is not None else None
+    sm.k_bar_dtype = _code(k_bar.dtype, "k_bar")
+    sm.v_bar_dtype = _code(v_bar.dtype, "v_bar")
+    bounds = summaries.get("k_max")
+    sm.bounds_dtype = _code(bounds.dtype if bounds is not None else torch.float32, "bounds")
+    sm.v_norm_max, sm.v_norm_all = vnm.data_ptr(), vna.data_ptr()
+    sm.counts = summaries["block_valid_counts"].data_ptr()
+    sm.nb = nb
+    sm.block_size = int(block_size)
+    return sm, nb
+
+
+def _sparse_decode_with_representatives(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, *, block_size,
+                                        scale, scales, summaries, out, out_dtype, workspace):
+    if pool_k.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("representatives need bf16 or fp32 K/V")
+    kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
+    _require_cuda(q, seq_lens, idx, n_sel)
+    hkv, d = int(pool_k.shape[1]), int(pool_k.shape[3])
+    sh = _decode_shape(q, hkv)
+    b = int(q.shape[0])
+    if q.shape[2] != d:
+        raise ValueError("q head_dim does not match the pool")
+    _check_i32(n_sel, "n_sel", (b, hkv))
+    if idx.dim() != 3 or tuple(idx.shape[:2]) != (b, hkv) or not idx.is_contiguous():
+        raise ValueError("idx must be a contiguous [B, Hkv, k_cap] int32 tensor")
+    _check_i32(idx, "idx")
+    if not n_sel.is_contiguous():
+        raise ValueError("n_sel must be contiguous")
+    if block_table is not None and block_table.shape[0] != b:
+        raise ValueError("block_table rows must match the batch")
+    sm, nb = _paged_summaries_desc(summaries, b, hkv, d, block_size)
+    scale = d ** -0.5 if scale is None else float(scale)
+    out = _out_tensor(q, out, out_dtype, workspace)
+    ws_dict = workspace if workspace is not None else {}
+    mask = workspace_tensor(ws_dict, "topk_block_mask", (b, hkv, max(nb, 1)), device=q.device, dtype=torch.uint8)
+    lib = N.lib()
+    N.check(lib.ia_topk_block_mask(idx.data_ptr(), n_sel.data_ptr(), int(idx.shape[2]), b, hkv, nb,
+                                   mask.data_ptr(), _stream(q)))
+    g = int(q.shape[1]) // hkv
+    ws_bytes = lib.ia_condition_workspace_size(b, hkv, g, d, nb, 0)
+    ws = _scratch(ws_dict, "hybrid_scratch", ws_bytes, q.device)
+    sfx = N.SuffixKV()
+    rc = lib.ia_fixed_mask_decode(sh, q.data_ptr(), sm, mask.data_ptr(), kv, sfx, scale, out.data_ptr(),
+                                  _code(out.dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
     N.check(rc)
     del keep
     return out

@@ -398,3 +398,54 @@ def test_fused_topk_decode_k_per_seq_and_fallback(device):
                                  wide, 0, block_size=block, k_per_seq=kvec, k_cap=k_cap, workspace={})
     torch.cuda.synchronize()
     assert torch.equal(out2, ref)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_sparse_decode_with_representatives(dt, device):
+    """Top-k finalize with representatives for the unselected blocks (logit
+    q.k_bar/sqrt(D) + log count, value v_bar: the external-mask hybrid of
+    fixed_mask.py:38-239) on a ragged paged batch, against the oracle's
+    fixed_mask_hybrid per sequence; with every block selected it equals the plain
+    top-k finalize."""
+    announce(f"sparse decode with representatives {dt}")
+    hq, hkv, d, page, block, k = 8, 2, 128, 16, 64, 5
+    lens = [1000, 3000, 70]
+    case = make_case(seed=515, batch=3, hq=hq, hkv=hkv, d=d, seq_lens=lens, page_size=page, dtype=dt)
+    tdt = _torch_dtype(dt)
+    dev = to_dev(case, device, dtype=tdt)
+    nb_max = max(math.ceil(L / block) for L in lens)
+    sdt = torch.float32 if dt == "f32" else torch.bfloat16
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max, full=True, k_bar_dtype=sdt, v_bar_dtype=sdt)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], summ["k_bar"], dev["seq_lens"], k, block_size=block, forced_last=1)
+    out = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block, include_representatives=True, summaries=summ,
+                                 out_dtype=torch.float32, workspace={})
+    # every block selected: no representative remains
+    all_idx = torch.arange(nb_max, device=device, dtype=torch.int32).expand(3, hkv, nb_max).contiguous()
+    all_n = torch.tensor([[math.ceil(L / block)] * hkv for L in lens], device=device, dtype=torch.int32)
+    full_r = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                    all_idx, all_n, block_size=block, include_representatives=True, summaries=summ,
+                                    out_dtype=torch.float32, workspace={})
+    full_p = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                    all_idx, all_n, block_size=block, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(full_r.cpu().numpy(), full_p.cpu().numpy(), atol=TOL[dt], rtol=0)
+    host = {key: summ[key].float().cpu().numpy() for key in ("k_bar", "v_bar")}
+    counts = summ["block_valid_counts"].cpu().numpy()
+    idx_h, n_h = idx.cpu().numpy(), n_sel.cpu().numpy()
+    got = out.cpu().numpy()
+    g = hq // hkv
+    for b, L in enumerate(lens):
+        nb = math.ceil(L / block)
+        kb = np.zeros((hkv, nb * block, d), np.float32)
+        vb = np.zeros((hkv, nb * block, d), np.float32)
+        kb[:, :L], vb[:, :L] = case["k"][b], case["v"][b]
+        sel = np.zeros((hkv, nb), bool)
+        for h in range(hkv):
+            sel[h, idx_h[b, h, :n_h[b, h]]] = True
+        ref = A.fixed_mask_hybrid(case["q"][b].reshape(hkv, g, 1, d), kb.reshape(hkv, nb, block, d),
+                                  vb.reshape(hkv, nb, block, d), counts[b, :nb], host["k_bar"][b, :, :nb],
+                                  host["v_bar"][b, :, :nb], sel, np.zeros((hkv, 0, d), np.float32),
+                                  np.zeros((hkv, 0, d), np.float32), emulate_bf16=(dt == "bf16"))
+        np.testing.assert_allclose(got[b], ref[:, :, 0].reshape(hq, d), atol=TOL[dt], rtol=0)

@@ -25,6 +25,7 @@ from .condition_block import _build_prompt_blocks, _condition_block_decode_outpu
 
 __all__ = [
     "ConditionBlockDecodeRunner",
+    "PagedTopkDecodeRunner",
     "condition_block_decode_context",
     "full_attention_sdpa_context",
     "model_attention_implementation",
@@ -247,6 +248,110 @@ class ConditionBlockDecodeRunner:
             self.stats_by_layer[int(layer_idx)] = stats
             _merge_stats_lazy(self.aggregate_stats, stats)
         return output.to(query.dtype), None
+
+
+class PagedTopkDecodeRunner:
+    """HF attention hook serving decode from a paged KV pool with the top-k rule (the
+    outer hook of ``ConditionBlockDecodeRunner``, CBT/core.py:1203-1355, with the
+    paged pool as its KV store; no reference counterpart).
+
+    Each layer owns a pool ``[n_pages, Hkv, page_size, D]`` in the model's dtype;
+    all layers share one block table ``[batch, ceil(max_seq_len / page_size)]`` (a
+    seeded permutation of the pages).  Prompt prefill runs torch SDPA and copies the
+    prompt's K/V into the pool, then builds the block summaries.  Every single-token
+    decode appends the new K/V row on the device (``append_kv``), refreshes the
+    summaries the new token touched (``update_block_summaries``) and runs the fused
+    top-k layer call (``sparse_topk_decode``); layers below ``full_attention_layers``
+    run the HIP paged dense decode.  Prompts of one batch share a length (no
+    padding).  Install with ``condition_block_decode_context(runner)``."""
+
+    def __init__(self, *, model, batch_size, max_seq_len, block_size, k, forced_first=0, forced_last=0,
+                 page_size=16, full_attention_layers=0, k_bar_dtype=None, seed=0):
+        from . import ops
+
+        self._ops = ops
+        cfg = model.config
+        param = next(model.parameters())
+        self.device, self.dtype = param.device, param.dtype
+        if self.dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError("the paged runner serves bf16 or fp32 models")
+        self.n_layers = int(cfg.num_hidden_layers)
+        self.n_kv_heads = int(cfg.num_key_value_heads)
+        self.head_dim = int(getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads)
+        self.batch_size, self.max_seq_len = int(batch_size), int(max_seq_len)
+        self.block_size, self.k = int(block_size), int(k)
+        self.forced_first, self.forced_last = int(forced_first), int(forced_last)
+        self.page_size = int(page_size)
+        self.full_attention_layers = int(full_attention_layers)
+        self.k_bar_dtype = k_bar_dtype or self.dtype
+        if self.block_size % 16 or self.page_size % 16:
+            raise ValueError("block_size and page_size must be multiples of 16")
+        self.nb_max = -(-self.max_seq_len // self.block_size)
+        pages_per_seq = -(-self.max_seq_len // self.page_size)
+        gen = torch.Generator(device="cpu").manual_seed(int(seed))
+        perm = torch.randperm(self.batch_size * pages_per_seq, generator=gen).to(torch.int32)
+        self.block_table = perm.view(self.batch_size, pages_per_seq).to(self.device)
+        shape = (self.batch_size * pages_per_seq, self.n_kv_heads, self.page_size, self.head_dim)
+        self.pools = [(torch.zeros(shape, device=self.device, dtype=self.dtype),
+                       torch.zeros(shape, device=self.device, dtype=self.dtype)) for _ in range(self.n_layers)]
+        # each layer advances its own lengths (append_kv moves them on the device)
+        self.seq_lens = [torch.zeros(self.batch_size, device=self.device, dtype=torch.int32)
+                         for _ in range(self.n_layers)]
+        self.old_seq_lens = [torch.zeros_like(t) for t in self.seq_lens]
+        self.summaries = [None] * self.n_layers
+        self.workspace_by_layer = [{} for _ in range(self.n_layers)]
+        self.module_to_layer_idx = {id(layer.self_attn): int(i) for i, layer in enumerate(model.model.layers)}
+
+    def _layer(self, module):
+        idx = getattr(module, "layer_idx", None)
+        return int(self.module_to_layer_idx[id(module)] if idx is None else idx)
+
+    def _fill(self, layer, key, value):
+        """Copy the prompt's K/V [B, Hkv, T, D] into the layer's pool, build summaries."""
+        b, hkv, t, d = key.shape
+        if b != self.batch_size or hkv != self.n_kv_heads or d != self.head_dim:
+            raise ValueError("prompt K/V do not match the runner's batch / heads / head_dim")
+        if t > self.max_seq_len:
+            raise ValueError("prompt longer than max_seq_len")
+        pk, pv = self.pools[layer]
+        n_pg = -(-t // self.page_size)
+        pages = self.block_table[:, :n_pg].reshape(-1).long()
+        for src, pool in ((key, pk), (value, pv)):
+            x = F.pad(src, (0, 0, 0, n_pg * self.page_size - t))
+            x = x.view(b, hkv, n_pg, self.page_size, d).permute(0, 2, 1, 3, 4)
+            pool[pages] = x.reshape(b * n_pg, hkv, self.page_size, d).to(pool.dtype)
+        self.seq_lens[layer].fill_(t)
+        if layer >= self.full_attention_layers:
+            self.summaries[layer] = self._ops.build_block_summaries(
+                pk, pv, self.block_table, self.seq_lens[layer], self.block_size, nb_max=self.nb_max,
+                k_bar_dtype=self.k_bar_dtype)
+
+    def hybrid_attention_forward(self, module, query, key, value, attention_mask, scaling, dropout=0.0, **kwargs):
+        layer = self._layer(module)
+        if query.shape[2] != 1:
+            self._fill(layer, key, value)
+            return _sdpa_prefill_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
+                                                   dropout=dropout, **kwargs)
+        if self.summaries[layer] is None and layer >= self.full_attention_layers:
+            raise ValueError("paged runner: decode before the prompt was prefilled")
+        ops = self._ops
+        pk, pv = self.pools[layer]
+        seq, old = self.seq_lens[layer], self.old_seq_lens[layer]
+        old.copy_(seq)
+        ops.append_kv(pk, pv, self.block_table, seq, key[:, :, -1].to(pk.dtype), value[:, :, -1].to(pv.dtype))
+        q = query[:, :, 0].contiguous()
+        ws = self.workspace_by_layer[layer]
+        if layer < self.full_attention_layers:
+            out = ops.paged_decode(q, pk, pv, self.block_table, seq, max_seq_len=self.max_seq_len, scale=scaling,
+                                   out_dtype=query.dtype, workspace=ws)
+        else:
+            summ = self.summaries[layer]
+            ops.update_block_summaries(summ, pk, pv, self.block_table, old, seq, self.block_size, max_new_tokens=1)
+            out = ops.sparse_topk_decode(q, pk, pv, self.block_table, seq, summ["k_bar"], self.k,
+                                         block_size=self.block_size, forced_first=self.forced_first,
+                                         forced_last=self.forced_last, scale=scaling, out_dtype=query.dtype,
+                                         workspace=ws)
+        return out.unsqueeze(1), None
 
 
 # ------------------------------------------------------------------ contexts

@@ -282,6 +282,40 @@ def test_fixed_mask_hybrid_vs_oracle(dt, device):
                                    err_msg=f"mask frac {frac}")
 
 
+def test_fixed_mask_clustered_selection(device):
+    """Clustered selections (all selected blocks contiguous inside one 256-block
+    route chunk, a different chunk per kv head) are split over the finalize's items
+    by count like spread ones: parity with the oracle for clustered, spread and
+    single-block masks over three route chunks."""
+    c = ("cluster", 41, 4, 4, 128, 64, 40000, 3, "bf16", False, "f32", False)
+    name, seed, hkv, g, d, b, p, s, *_ = c
+    announce("fixed-mask clustered selections")
+    host, dev = _make(c, device)
+    prefix = cb._build_prompt_blocks(dev["k"], dev["v"], b)
+    pre = _prefix_np(prefix)
+    nb = pre["block_valid_counts"].shape[0]
+    assert nb > 2 * 256
+    masks = {}
+    m = np.zeros((hkv, nb), bool)
+    for h in range(hkv):
+        start = 30 + 256 * (h % 3)
+        m[h, start:start + 60] = True
+    masks["clustered"] = m
+    masks["spread"] = np.zeros((hkv, nb), bool)
+    masks["spread"][:, ::10] = True
+    masks["single"] = np.zeros((hkv, nb), bool)
+    masks["single"][:, nb - 1] = True
+    for label, mask in masks.items():
+        out = cb.fixed_mask_hybrid_attention(q_grouped=dev["q"], prompt_prefix=prefix,
+                                             selected=torch.from_numpy(mask).to(device), k_suffix=dev["ks"],
+                                             v_suffix=dev["vs"], block_size=b, output_dtype=torch.float32)
+        torch.cuda.synchronize()
+        exp = A.fixed_mask_hybrid(host["q"], _padded(host["k"], b), _padded(host["v"], b),
+                                  pre["block_valid_counts"], pre["k_bar"], pre["v_bar"], mask, host["ks"],
+                                  host["vs"], emulate_bf16=True)
+        np.testing.assert_allclose(_np(out), exp, atol=TOL["bf16"], rtol=0, err_msg=label)
+
+
 def test_condition_contract_errors(device):
     announce("condition contract errors")
     k = torch.zeros((2, 100, 64), device=device, dtype=torch.bfloat16)

@@ -498,11 +498,15 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     int row;  // first row within the page (suffix: first suffix token)
     int nv;   // valid rows, 1..16
   };
-  // (wave-uniform: kept in scalar registers)
+  // (wave-uniform: kept in scalar registers).  Past the list the iterator names row 0
+  // of subtile 0 with no valid rows: the ring's loads stay unconditional (the same
+  // count on every path, so the compiler's memory-counter waits stay exact) and
+  // touch one row already read.  Requires n_sub >= 1.
   auto seek = [&](int k) -> Sub {
-    if (k >= n_sub) return Sub{n_sub, 0, 0, 0};
-    const int info = __builtin_amdgcn_readfirstlane(sub_info[k]);
-    return Sub{k, __builtin_amdgcn_readfirstlane(sub_pg[k]), info >> 5, info & 31};
+    const int kc = k < n_sub ? k : 0;
+    const int info = __builtin_amdgcn_readfirstlane(sub_info[kc]);
+    const int pg = __builtin_amdgcn_readfirstlane(sub_pg[kc]);
+    return k < n_sub ? Sub{k, pg, info >> 5, info & 31} : Sub{n_sub, pg, info >> 5, 0};
   };
   auto next = [&](const Sub& c) -> Sub { return seek(c.k + kFinWaves); };
 
@@ -523,18 +527,38 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
   };
 
+  // fp8 pages: the (K, V) scales of the subtile's page, loaded unconditionally (the
+  // suffix source, which has none, reads a word of its own row; consume uses 1)
+  auto page_scales = [&](const Sub& sb, const char* kp, u32 (&xb)[2]) {
+    if constexpr (kFp8) {
+      const bool paged = sb.pg >= 0;
+      const int64_t at = (int64_t)sb.pg * kv.scale_page_stride + h;
+      xb[0] = *(paged ? reinterpret_cast<const u32*>(kv.k_scale + at) : reinterpret_cast<const u32*>(kp));
+      xb[1] = *(paged ? reinterpret_cast<const u32*>(kv.v_scale + at) : reinterpret_cast<const u32*>(kp));
+    }
+  };
+
   // ---- software pipeline over a ring of NBUF register buffers: while subtile n
-  // is consumed, subtiles n+1 .. n+NBUF-1 are in flight
+  // is consumed, subtiles n+1 .. n+NBUF-1 are in flight.  Everything a subtile
+  // reads from memory (rows, and an fp8 page's two scales in xbuf) is loaded by its
+  // issue: a load issued by consume would make the wave wait for every load in
+  // flight (the vector memory counter drains in order).
   auto stream = [&](auto&& issue, auto&& consume) {
     constexpr int NBUF = KV::kRing;
-    u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD];
+    u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD], xbuf[NBUF][2];
     Sub ring[NBUF];
+    if (n_sub == 0) return;
     ring[0] = seek(wave);
-    issue(ring[0], kbuf[0], vbuf[0]);
+    issue(ring[0], kbuf[0], vbuf[0], xbuf[0]);
+    // the loads stay in ring order and ahead of the work on older subtiles (no
+    // instruction crosses a scheduling barrier): the wait for subtile n then leaves
+    // the loads of n+1 .. in flight
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 1; k < NBUF - 1; ++k) {
       ring[k] = next(ring[k - 1]);
-      issue(ring[k], kbuf[k], vbuf[k]);
+      issue(ring[k], kbuf[k], vbuf[k], xbuf[k]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     bool done = false;
     int n_done = 0;
@@ -548,8 +572,9 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
           break;
         }
         ring[fk] = next(ring[pk]);
-        issue(ring[fk], kbuf[fk], vbuf[fk]);
-        consume(ring[k], kbuf[k], vbuf[k]);
+        issue(ring[fk], kbuf[fk], vbuf[fk], xbuf[fk]);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(ring[k], kbuf[k], vbuf[k], xbuf[k]);
         // the two waves of a SIMD (w, w ^ 4) stream equal shares, but issue
         // arbitration favours the older one; the wave ahead yields priority so
         // both finish together (the assignment, hence the result, is unchanged)
@@ -589,12 +614,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     for (int n = 0; n < DPL; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = kNegInf, l_run = 0.f;
 
-    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
-      if (sb.k >= n_sub) return;
+    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
       const char* kp;
       const char* vp;
       int64_t kts, vts;
       sub_rows(sb, kp, vp, kts, vts);
+      page_scales(sb, kp, xb);
       // K: token rho (row 0 past the valid rows), NWD 16-byte pieces at 64*pc + 16*r
       const char* kr = kp + (int64_t)(rho < sb.nv ? rho : 0) * kts + 16 * r;
 #pragma unroll
@@ -612,7 +637,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     };
 
-    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
       auto kword = [&](int fw) -> u32 { return kb[fw / NWD][fw % NWD]; };
       // ---------------- scores: token r + 4i, query row c16 % G, in accumulator i
       f32x4_t s = {0.f, 0.f, 0.f, 0.f};
@@ -635,8 +660,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       float vsc = 1.f;
       if constexpr (kFp8) {
         if (sb.pg >= 0) {
-          sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
-          vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+          sc *= __uint_as_float(xb[0]);
+          vsc = __uint_as_float(xb[1]);
         }
       }
       // ---------------- online softmax, one update per subtile (max over the 16
@@ -764,12 +789,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
 #pragma unroll
       for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
 
-    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD]) {
-      if (sb.k >= n_sub) return;
+    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
       const char* kp;
       const char* vp;
       int64_t kts, vts;
       sub_rows(sb, kp, vp, kts, vts);
+      page_scales(sb, kp, xb);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // rows past the subtile's valid rows re-read its first row (always valid); their weights are zero
@@ -779,7 +804,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     };
 
-    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD]) {
+    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
       // fp8 rows widened to bf16 pairs (exact: every e4m3 value is a bf16 value)
       u32 kx[4][NWB], vx[4][NWB];
 #pragma unroll
@@ -828,8 +853,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       float vsc = 1.f;
       if constexpr (kFp8) {
         if (sb.pg >= 0) {
-          sc *= kv.k_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
-          vsc = kv.v_scale[(int64_t)sb.pg * kv.scale_page_stride + h];
+          sc *= __uint_as_float(xb[0]);
+          vsc = __uint_as_float(xb[1]);
         }
       }
       const bool valid = 4 * my_step + r < sb.nv;

@@ -81,19 +81,19 @@ struct RawRow {
     if constexpr (BF16) {
       const unsigned short* p = reinterpret_cast<const unsigned short*>(base) + off;
       if constexpr (DPL == 8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        const u32x4_t v = ld_stream16(p);
+        w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
       } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        w[0] = v.x; w[1] = v.y;
+        const u32x2_t v = ld_stream8(p);
+        w[0] = v[0]; w[1] = v[1];
       }
     } else {
       const float* p = reinterpret_cast<const float*>(base) + off;
 #pragma unroll
       for (int e = 0; e < DPL; e += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(p + e);
-        w[e] = __float_as_uint(v.x); w[e + 1] = __float_as_uint(v.y);
-        w[e + 2] = __float_as_uint(v.z); w[e + 3] = __float_as_uint(v.w);
+        const u32x4_t v = ld_stream16(p + e);
+        w[e] = v[0]; w[e + 1] = v[1];
+        w[e + 2] = v[2]; w[e + 3] = v[3];
       }
     }
   }

@@ -58,21 +58,22 @@ struct KvFp8 {
   static constexpr int kRing = 3;
 };
 
+// NWD words of one K/V row slice, as streaming loads
 template <int NWD>
 __device__ __forceinline__ void load_words(const char* p, u32* w) {
   if constexpr (NWD == 8) {
-    const uint4 a = reinterpret_cast<const uint4*>(p)[0];
-    const uint4 b = reinterpret_cast<const uint4*>(p)[1];
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    const u32x4_t a = ld_stream16(p);
+    const u32x4_t b = ld_stream16(p + 16);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+    w[4] = b[0]; w[5] = b[1]; w[6] = b[2]; w[7] = b[3];
   } else if constexpr (NWD == 4) {
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    const u32x4_t a = ld_stream16(p);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
   } else if constexpr (NWD == 2) {
-    const uint2 a = *reinterpret_cast<const uint2*>(p);
-    w[0] = a.x; w[1] = a.y;
+    const u32x2_t a = ld_stream8(p);
+    w[0] = a[0]; w[1] = a[1];
   } else {
-    w[0] = *reinterpret_cast<const u32*>(p);
+    w[0] = ld_stream4(p);
   }
 }
 
@@ -624,8 +625,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       const char* kr = kp + (int64_t)(rho < sb.nv ? rho : 0) * kts + 16 * r;
 #pragma unroll
       for (int pc = 0; pc < NWD; ++pc) {
-        const uint4 a = *reinterpret_cast<const uint4*>(kr + 64 * pc);
-        const u32 w4[4] = {a.x, a.y, a.z, a.w};
+        const u32x4_t a = ld_stream16(kr + 64 * pc);
+        const u32 w4[4] = {a[0], a[1], a[2], a[3]};
 #pragma unroll
         for (int e = 0; e < 4; ++e) kb[(4 * pc + e) / NWD][(4 * pc + e) % NWD] = w4[e];
       }

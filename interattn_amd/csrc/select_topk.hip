@@ -94,12 +94,12 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
         if constexpr (NWR >= 4) {
 #pragma unroll
           for (int v4 = 0; v4 < NWR; v4 += 4) {
-            const uint4 x = reinterpret_cast<const uint4*>(rowp)[v4 / 4];
-            w[t][v4] = x.x; w[t][v4 + 1] = x.y; w[t][v4 + 2] = x.z; w[t][v4 + 3] = x.w;
+            const u32x4_t x = ld_stream16(rowp + 4 * v4);
+            w[t][v4] = x[0]; w[t][v4 + 1] = x[1]; w[t][v4 + 2] = x[2]; w[t][v4 + 3] = x[3];
           }
         } else {
-          const uint2 x = *reinterpret_cast<const uint2*>(rowp);
-          w[t][0] = x.x; w[t][1] = x.y;
+          const u32x2_t x = ld_stream8(rowp);
+          w[t][0] = x[0]; w[t][1] = x[1];
         }
       } else {
 #pragma unroll
@@ -175,12 +175,12 @@ __global__ __launch_bounds__(256) void ia_condition_block_topk_scores(SelectPara
       if constexpr (NWR >= 4) {
 #pragma unroll
         for (int v4 = 0; v4 < NWR; v4 += 4) {
-          const uint4 x = reinterpret_cast<const uint4*>(rowp)[v4 / 4];
-          w[t][v4] = x.x; w[t][v4 + 1] = x.y; w[t][v4 + 2] = x.z; w[t][v4 + 3] = x.w;
+          const u32x4_t x = ld_stream16(rowp + 4 * v4);
+          w[t][v4] = x[0]; w[t][v4 + 1] = x[1]; w[t][v4 + 2] = x[2]; w[t][v4 + 3] = x[3];
         }
       } else {
-        const uint2 x = *reinterpret_cast<const uint2*>(rowp);
-        w[t][0] = x.x; w[t][1] = x.y;
+        const u32x2_t x = ld_stream8(rowp);
+        w[t][0] = x[0]; w[t][1] = x[1];
       }
     } else {
 #pragma unroll

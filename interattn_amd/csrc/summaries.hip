@@ -40,18 +40,18 @@ __device__ __forceinline__ void load_dims(const char* p, float* out) {
   if constexpr (EB == 4) {
 #pragma unroll
     for (int e = 0; e < DPL; e += 4) {
-      const uint4 a = reinterpret_cast<const uint4*>(p)[e / 4];
-      out[e] = __uint_as_float(a.x); out[e + 1] = __uint_as_float(a.y);
-      out[e + 2] = __uint_as_float(a.z); out[e + 3] = __uint_as_float(a.w);
+      const u32x4_t a = ld_stream16(p + 4 * e);
+      out[e] = __uint_as_float(a[0]); out[e + 1] = __uint_as_float(a[1]);
+      out[e + 2] = __uint_as_float(a[2]); out[e + 3] = __uint_as_float(a[3]);
     }
   } else if constexpr (EB == 2) {
     u32 w[DPL / 2];
     if constexpr (DPL == 8) {
-      const uint4 a = *reinterpret_cast<const uint4*>(p);
-      w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+      const u32x4_t a = ld_stream16(p);
+      w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
     } else {
-      const uint2 a = *reinterpret_cast<const uint2*>(p);
-      w[0] = a.x; w[1] = a.y;
+      const u32x2_t a = ld_stream8(p);
+      w[0] = a[0]; w[1] = a[1];
     }
 #pragma unroll
     for (int e = 0; e < DPL / 2; ++e) {
@@ -61,10 +61,10 @@ __device__ __forceinline__ void load_dims(const char* p, float* out) {
   } else {
     u32 w[DPL / 4];
     if constexpr (DPL == 8) {
-      const uint2 a = *reinterpret_cast<const uint2*>(p);
-      w[0] = a.x; w[1] = a.y;
+      const u32x2_t a = ld_stream8(p);
+      w[0] = a[0]; w[1] = a[1];
     } else {
-      w[0] = *reinterpret_cast<const u32*>(p);
+      w[0] = ld_stream4(p);
     }
 #pragma unroll
     for (int e = 0; e < DPL / 4; ++e) fp8x4_to_f32(w[e], out + 4 * e);

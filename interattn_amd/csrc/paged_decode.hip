@@ -9,9 +9,18 @@ namespace ia {
 
 int units_cap_items(int64_t units) { return (int)std::max<int64_t>(1, std::min<int64_t>(units, kMaxItemsPerBh)); }
 
+// Split-K workspace: (m, l) partials, accumulator partials, items per row.
 size_t decode_ws_size(int batch, int hkv, int group, int d, int max_items) {
   const size_t bh = (size_t)batch * hkv;
-  return align_up(bh * max_items * group * 2 * 4, 256) + bh * max_items * group * d * 4;
+  return align_up(bh * max_items * group * 2 * 4, 256) + align_up(bh * max_items * group * d * 4, 256) + bh * 4;
+}
+
+void set_decode_ws(DecodeParams& p, char* ws, int64_t bh, int max_items, int group, int d) {
+  const size_t ml = align_up((size_t)bh * max_items * group * 2 * 4, 256);
+  const size_t acc = align_up((size_t)bh * max_items * group * d * 4, 256);
+  p.part_ml = reinterpret_cast<float*>(ws);
+  p.part_acc = reinterpret_cast<float*>(ws + ml);
+  p.part_n = reinterpret_cast<int32_t*>(ws + ml + acc);
 }
 
 int check_kv(const ia_paged_kv* kv, int d) {
@@ -60,6 +69,27 @@ int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, 
   }
   if (p.q_f32) return fail(IA_ERR_UNSUPPORTED, "fp8 kv needs bf16 q");
   return dispatch_fp8(p, d, g, src, grid, st, resident);
+}
+
+int balanced_grid(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t n_rows, int64_t units_max,
+                  int nsub_u, int cap_items, hipStream_t st, int* grid_out, int* budget_out) {
+  int resident = 0;
+  int rc = dispatch_decode(p, kv_dtype, d, g, src, dim3(1), st, &resident);
+  if (rc) return rc;
+  if (resident <= 0) resident = 1024;
+  // an item's unit ranges and subtile list live in LDS: at most t_cap raw slots
+  const int64_t t_cap = plan_t_cap(nsub_u);
+  const int64_t s_cap = units_max * nsub_u;
+  if (s_cap > (int64_t)cap_items * t_cap)
+    return fail(IA_ERR_UNSUPPORTED, "sequence too long for one launch: " + std::to_string(units_max) + " units");
+  if (n_rows > kPlanMaxRows)
+    return fail(IA_ERR_UNSUPPORTED, "batch x kv heads above " + std::to_string(kPlanMaxRows) + " rows for one launch");
+  int64_t grid = n_rows;  // one item per row when the partials have a single slot
+  if (cap_items > 1)
+    grid = std::max<int64_t>(std::max<int64_t>(resident, n_rows), n_rows * ((s_cap + t_cap - 1) / t_cap));
+  *grid_out = (int)grid;
+  *budget_out = resident;
+  return IA_OK;
 }
 
 int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
@@ -139,26 +169,31 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
 
   const int64_t bh = (int64_t)shape->batch * shape->n_kv_heads;
   const int src = sparse ? kSrcTopk : kSrcDense;
-  int items = 1;
-  rc = decode_items(p, kv->dtype, D, G, src, bh, units_max, (unit_tokens + 15) / 16, cap_items, st, &items);
-  if (rc) return rc;
   p.max_items = cap_items;  // stride of the partials; items per (b, h) never exceed it
-
-  char* ws = reinterpret_cast<char*>(workspace);
-  const size_t nbh = (size_t)bh;
-  if (ws) {
-    p.part_ml = reinterpret_cast<float*>(ws);
-    p.part_acc = reinterpret_cast<float*>(ws + align_up(nbh * cap_items * G * 2 * 4, 256));
-  }
-  dim3 grid(items, shape->n_kv_heads, shape->batch);
-  return dispatch_decode(p, kv->dtype, D, G, src, grid, st, nullptr);
+  int grid = 0;
+  rc = balanced_grid(p, kv->dtype, D, G, src, bh, units_max, (unit_tokens + 15) / 16, cap_items, st, &grid,
+                     &p.plan_budget);
+  if (rc) return rc;
+  p.n_rows = (int)bh;
+  if (workspace) set_decode_ws(p, reinterpret_cast<char*>(workspace), bh, cap_items, G, D);
+  return dispatch_decode(p, kv->dtype, D, G, src, dim3(grid), st, nullptr);
 }
 
-// Fused top-k decode workspace: the score rows, then the split-K partials.
-size_t fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, size_t* decode_off) {
+// Plan entries a fused launch may need: its grid is at most the resident workgroups
+// (below kPlanMinEntries on any device this build targets) or n_rows x
+// ceil(s_cap / t_cap) <= n_rows x max_items when LDS bounds force small items.
+constexpr int64_t kPlanMinEntries = 4096;
+int64_t fused_plan_entries(int64_t n_rows, int k_cap) {
+  return std::max<int64_t>(kPlanMinEntries, n_rows * units_cap_items(k_cap));
+}
+
+// Fused top-k decode workspace: the score rows, the split-K partials, the plan.
+size_t fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, size_t* decode_off,
+                       size_t* plan_off) {
   const size_t scores = align_up((size_t)batch * hkv * std::max(nb_max, 1) * 4, 256);
   *decode_off = scores;
-  return scores + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap));
+  *plan_off = align_up(scores + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap)), 256);
+  return *plan_off + (size_t)fused_plan_entries((int64_t)batch * hkv, k_cap) * sizeof(PlanEntry);
 }
 
 int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
@@ -188,8 +223,8 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
                                         "; use ia_select_topk + ia_sparse_paged_decode");
   const int G = shape->n_q_heads / shape->n_kv_heads;
   const int D = shape->head_dim;
-  size_t decode_off = 0;
-  const size_t need = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, &decode_off);
+  size_t decode_off = 0, plan_off = 0;
+  const size_t need = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, &decode_off, &plan_off);
   if (!workspace || workspace_bytes < need)
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
@@ -197,11 +232,6 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = reinterpret_cast<char*>(workspace);
   float* scores = reinterpret_cast<float*>(ws);
-  if (nb_max > 0) {
-    rc = run_topk_scores(shape, q, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride, seq_lens, block_size,
-                         nb_max, scores, st);
-    if (rc) return rc;
-  }
 
   DecodeParams p{};
   p.q = q;
@@ -227,14 +257,23 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   p.out = out;
   const int cap_items = units_cap_items(k_cap);
   const int64_t bh = (int64_t)shape->batch * shape->n_kv_heads;
-  int items = 1;
-  rc = decode_items(p, kv->dtype, D, G, kSrcTopkFused, bh, k_cap, block_size / 16, cap_items, st, &items);
-  if (rc) return rc;
   p.max_items = cap_items;
-  p.part_ml = reinterpret_cast<float*>(ws + decode_off);
-  p.part_acc = reinterpret_cast<float*>(ws + decode_off + align_up((size_t)bh * cap_items * G * 2 * 4, 256));
-  return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(items, shape->n_kv_heads, shape->batch), st,
-                         nullptr);
+  int grid = 0;
+  rc = balanced_grid(p, kv->dtype, D, G, kSrcTopkFused, bh, k_cap, block_size / 16, cap_items, st, &grid,
+                     &p.plan_budget);
+  if (rc) return rc;
+  if (grid > fused_plan_entries(bh, k_cap)) return fail(IA_ERR_UNSUPPORTED, "plan entries exceed the workspace");
+  p.n_rows = (int)bh;
+  set_decode_ws(p, ws + decode_off, bh, cap_items, G, D);
+  PlanEntry* entries = reinterpret_cast<PlanEntry*>(ws + plan_off);
+  p.plan = entries;
+  // the scorer launch also writes the finalize's plan
+  const TopkPlanArgs plan{k, k_per_seq, forced_first, forced_last, forced_in_k, k_cap,
+                          entries, grid, p.plan_budget, cap_items, (int)bh};
+  rc = run_topk_scores(shape, q, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride, seq_lens, block_size,
+                       nb_max, scores, plan, st);
+  if (rc) return rc;
+  return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(grid), st, nullptr);
 }
 
 }  // namespace
@@ -244,8 +283,8 @@ extern "C" {
 
 size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
                                             int32_t nb_max, int32_t k_cap) {
-  size_t decode_off = 0;
-  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1), &decode_off);
+  size_t decode_off = 0, plan_off = 0;
+  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1), &decode_off, &plan_off);
 }
 
 int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,

@@ -39,6 +39,9 @@
 //   the weight before its bf16 rounding.
 #pragma once
 
+#include <algorithm>
+
+#include "plan.hpp"
 #include "topk_select.hpp"
 
 namespace ia {
@@ -87,6 +90,9 @@ constexpr int kFusedMaxBlocks = 4096;  // score row staged in LDS by the fused t
 constexpr int kRouteChunk = 256;      // blocks per route workgroup (condition mode)
 constexpr int kMaxRouteChunks = 256;  // route chunks per (sequence, kv head)
 constexpr int kMaxItemsPerBh = 64;  // upper bound of split-K items per (sequence, kv head)
+// Sources whose launch is planned by work (one flat grid, items per (sequence, kv
+// head) in proportion to its subtiles); kSrcLists keeps a fixed item count per row.
+constexpr bool src_balanced(int src) { return src != kSrcLists; }
 constexpr int kSpecEntries = 2048;  // list entries a finalize item stages without waiting for the counts
 constexpr int kNoPage = -1;
 constexpr int kSfxPage = -2;          // subtile of the contiguous suffix source
@@ -130,6 +136,13 @@ struct DecodeParams {
   void* out;
   float* part_ml;  // [batch*Hkv, max_items, G, 2]
   float* part_acc; // [batch*Hkv, max_items, G, D]
+  // balanced sources: items of each (b, h) row, written by the row's item 0 and
+  // read by the merge; the plan's workgroup budget and the row count; the fused
+  // top-k source reads its plan entries (one per workgroup) from the scorer launch
+  int32_t* part_n;  // [batch*Hkv]
+  int32_t plan_budget;
+  int32_t n_rows;
+  const PlanEntry* plan;
 };
 
 constexpr int kWaves = 4;  // split-K merge
@@ -139,8 +152,8 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kFinWaves = 8;
 constexpr int kFinThreads = kFinWaves * 64;
 constexpr int kDenseTile = 128;
-constexpr int kMaxUnitsPerItem = 512;  // LDS unit ranges per item
-constexpr int kMaxSubsPerItem = 2048;  // LDS page ids per item (16 tokens each)
+constexpr int kMaxUnitsPerItem = kPlanMaxUnits;  // LDS unit ranges per item
+constexpr int kMaxSubsPerItem = kPlanMaxSubs;  // LDS page ids per item (16 tokens each)
 
 // Lane (within the 16-lane row) and slot holding the reduce-scattered value of
 // index x = i*G + g (see reduce_scatter16).
@@ -250,6 +263,18 @@ __device__ __forceinline__ float mfma_row_alpha(float alpha, int i, int lane) {
   }
 }
 
+// ------------------------------------------------------------ balanced launch plan
+// (plan.hpp).  Units of row r for the finalize's own plan: top-k, the row's selected
+// blocks; dense, its 128-token tiles.
+template <int SRC>
+__device__ __forceinline__ int plan_row_units(const DecodeParams& p, int r) {
+  if constexpr (SRC == kSrcTopk) {
+    return min(max(p.n_sel[r], 0), p.k_cap);
+  } else {
+    return cdiv_pos(max(p.seq_lens[r / p.n_kv_heads], 0), p.unit_tokens);
+  }
+}
+
 template <int D, int G, typename KV, int SRC>
 __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
@@ -282,19 +307,60 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ float wm_lds[kFinWaves][G];
   __shared__ float wl_lds[kFinWaves][G];
 
+  __shared__ PlanEntry plan_lds;
+
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c16 = lane & 15;
   const int r = lane >> 4;
-  const int item = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
-  const int bh = b * p.n_kv_heads + h;
+  constexpr bool kBalanced = src_balanced(SRC);
+  const int nsub_u = ((SRC == kSrcLists ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
   if (threadIdx.x < kFinWaves) wprog[threadIdx.x] = 0;  // read after the prologue's barriers
 
+  // ---- this workgroup's (b, h) row and its item: from the launch plan (balanced
+  // sources; the fused top-k plan comes from the scorer launch), else from the grid
+  int b, h, item, n_items_row = 1, slot_lo = 0, slot_hi = 0, seq_len = 0, n_units = 0, n_blk_units = 0, sfx_len = 0;
+  int k_b = p.topk_k;
+  if constexpr (kBalanced) {
+    PlanEntry e;
+    if constexpr (SRC == kSrcTopkFused) {
+      e = p.plan[blockIdx.x];
+    } else {
+      if (wave == 0) {
+        PlanRows rows;
+        auto slots_of = [&](int rr) -> int { return plan_row_units<SRC>(p, rr) * nsub_u; };
+        const int t = plan_t_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
+        const PlanEntry pe = plan_entry_wave(slots_of, rows, p.n_rows, t, (int)blockIdx.x, nsub_u);
+        if (lane == 0) plan_lds = pe;
+      }
+      __syncthreads();
+      e = plan_lds;
+    }
+    const int row = __builtin_amdgcn_readfirstlane(e.row);
+    if (row < 0) return;  // idle workgroup (the whole workgroup)
+    b = row / p.n_kv_heads;
+    h = row - b * p.n_kv_heads;
+    item = __builtin_amdgcn_readfirstlane(e.item);
+    n_items_row = __builtin_amdgcn_readfirstlane(e.n_items);
+    slot_lo = __builtin_amdgcn_readfirstlane(e.slot_lo);
+    slot_hi = __builtin_amdgcn_readfirstlane(e.slot_hi);
+    n_units = __builtin_amdgcn_readfirstlane(e.n_units);
+    if constexpr (SRC == kSrcTopkFused) {
+      seq_len = __builtin_amdgcn_readfirstlane(e.seq_len);
+      k_b = __builtin_amdgcn_readfirstlane(e.k_row);
+    } else {
+      seq_len = max(p.seq_lens[b], 0);
+    }
+  } else {
+    b = blockIdx.z;
+    h = blockIdx.y;
+    item = blockIdx.x;
+  }
+  const int bh = b * p.n_kv_heads + h;
+
   // ---- query rows of this kv head: raw loads issued first (independent of the
-  // prologue), converted after it.  Vector path: every row at the lane's dim slice
-  // c16*DPL ..; MFMA path: row c16 % G at the dims of the lane's k-slices.
+  // rest of the prologue), converted after it.  Vector path: every row at the lane's
+  // dim slice c16*DPL ..; MFMA path: row c16 % G at the dims of the lane's k-slices.
   constexpr int QR0 = kMfma ? kMfmaK : G;
   constexpr int QR1 = kMfma ? 8 : DPL;
   u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs (upper half unused)
@@ -317,16 +383,11 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
   }
 
-  const int seq_len = (SRC == kSrcLists) ? 0 : max(p.seq_lens[b], 0);
-  int n_units, n_blk_units = 0, sfx_len = 0;
-  if constexpr (SRC == kSrcTopk) {
-    n_units = min(max(p.n_sel[bh], 0), p.k_cap);
-  } else if constexpr (SRC == kSrcTopkFused) {
+  if constexpr (SRC == kSrcTopkFused) {
     // the whole score row in LDS, then the shared top-k rule (every item of the row
     // selects the same blocks; item 0 publishes them)
-    const int nbs = min((seq_len + p.unit_tokens - 1) / p.unit_tokens, p.nb_max);
+    const int nbs = min(cdiv_pos(seq_len, p.unit_tokens), p.nb_max);
     const float* sc_row = p.scores + (int64_t)bh * p.nb_max;
-    const int k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
     // staging the row also gives the selection its candidates' key range
     const TopkForced forced(rule, nbs);
@@ -342,15 +403,14 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
     topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
     __syncthreads();
-    n_units = topk_select<kFinThreads, true>(
+    const int n_chosen = topk_select<kFinThreads, true>(
         ftk, [&](int j) -> u32 { return order_key(fsc[j]); }, nbs, rule, [&](int pos, int j) { fsel[pos] = j; });
     if (item == 0 && p.idx_out) {
-      for (int t = threadIdx.x; t < n_units; t += kFinThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
-      if (threadIdx.x == 0) p.n_sel_out[bh] = n_units;
+      for (int t = threadIdx.x; t < n_chosen; t += kFinThreads) p.idx_out[(int64_t)bh * p.k_cap + t] = fsel[t];
+      if (threadIdx.x == 0) p.n_sel_out[bh] = n_chosen;
     }
-  } else if constexpr (SRC == kSrcDense) {
-    n_units = (seq_len + p.unit_tokens - 1) / p.unit_tokens;
-  } else {
+    n_units = min(n_units, n_chosen);  // equal: the plan counts with the same rule
+  } else if constexpr (SRC == kSrcLists) {
     // selected blocks of every route chunk (exclusive prefix in LDS), then the suffix tiles.
     // With few route chunks every list entry is staged in the same round trip as the
     // counts (entries past a chunk's count are never used).
@@ -379,33 +439,44 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     sfx_len = p.sfx_len ? min(max(p.sfx_len[(int64_t)b * p.sfx_len_stride], 0), p.sfx_cap) : 0;
     n_units = n_blk_units + (sfx_len + kDenseTile - 1) / kDenseTile;
   }
-  // units are spread evenly over the row's items
-  const int upi = max(1, (n_units + (int)gridDim.x - 1) / (int)gridDim.x);
-  const int n_items = max(1, (n_units + upi - 1) / upi);
-  const bool split = gridDim.x > 1 || p.rep_ml != nullptr;  // partials + merge kernel
-  if (item >= n_items) {
-    // an empty slot: the merge reads every slot of the grid row
-    if (threadIdx.x < G) {
-      const int64_t slot = (int64_t)bh * p.max_items + item;
-      p.part_ml[(slot * G + threadIdx.x) * 2 + 0] = kNegInf;
-      p.part_ml[(slot * G + threadIdx.x) * 2 + 1] = 0.f;
+  bool split;
+  int u_begin, nu;
+  if constexpr (kBalanced) {
+    // the plan's raw slots [slot_lo, slot_hi) lie in units [u_begin, u_begin + nu)
+    split = n_items_row > 1;
+    u_begin = slot_lo / nsub_u;
+    nu = slot_hi > slot_lo ? cdiv_pos(slot_hi, nsub_u) - u_begin : 0;
+    if (item == 0 && threadIdx.x == 0 && p.part_n) p.part_n[bh] = n_items_row;
+  } else {
+    // units are spread evenly over the row's items
+    const int upi = max(1, (n_units + (int)gridDim.x - 1) / (int)gridDim.x);
+    const int n_items = max(1, (n_units + upi - 1) / upi);
+    split = gridDim.x > 1 || p.rep_ml != nullptr;  // partials + merge kernel
+    if (item >= n_items) {
+      // an empty slot: the merge reads every slot of the grid row
+      if (threadIdx.x < G) {
+        const int64_t slot = (int64_t)bh * p.max_items + item;
+        p.part_ml[(slot * G + threadIdx.x) * 2 + 0] = kNegInf;
+        p.part_ml[(slot * G + threadIdx.x) * 2 + 1] = 0.f;
+      }
+      return;
     }
-    return;
+    u_begin = item * upi;
+    nu = max(0, min(n_units, u_begin + upi) - u_begin);
+    slot_lo = u_begin * nsub_u;
+    slot_hi = (u_begin + nu) * nsub_u;
   }
 
   const ia_paged_kv& kv = p.kv;
   const int page_size = kv.page_size;
   const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
-  const int u_begin = item * upi;
-  const int nu = max(0, min(n_units, u_begin + upi) - u_begin);
-  const int nsub_u = ((SRC == kSrcLists ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
 
   // ---- prologue: token ranges of this item's units, then one page id per subtile
   for (int t = threadIdx.x; t < nu; t += kFinThreads) {
     const int u = u_begin + t;
     int lo = 0, hi = 0, sfx = 0;
     if constexpr (SRC == kSrcTopk || SRC == kSrcTopkFused) {
-      const int j = (SRC == kSrcTopkFused) ? fsel[u] : p.idx[(int64_t)bh * p.k_cap + u];
+      const int j = u >= n_units ? -1 : (SRC == kSrcTopkFused) ? fsel[u] : p.idx[(int64_t)bh * p.k_cap + u];
       if (j >= 0 && (int64_t)j * p.unit_tokens < seq_len) {
         lo = j * p.unit_tokens;
         hi = min(lo + p.unit_tokens, seq_len);
@@ -440,12 +511,14 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     unit_hi[t] = sfx ? -hi - 1 : hi;  // suffix units carry a negative end
   }
   __syncthreads();
-  // valid subtiles of the item in ascending order, compacted (ballots + per-wave counts)
+  // valid subtiles of the item's raw slots in ascending order, compacted (ballots +
+  // per-wave counts)
   int n_sub = 0;  // uniform
+  const int raw0 = u_begin * nsub_u;
   for (int t0 = 0; t0 < nu * nsub_u; t0 += kFinThreads) {
     const int t = t0 + threadIdx.x;
     int pg = kNoPage, info = 0;
-    if (t < nu * nsub_u) {
+    if (t < nu * nsub_u && raw0 + t >= slot_lo && raw0 + t < slot_hi) {
       const int u = t / nsub_u;
       const int lo = unit_lo[u];
       const int hi_raw = unit_hi[u];
@@ -994,6 +1067,10 @@ constexpr int kMergeFastSlots = 8;  // up to this many slots: one round trip, on
 // one wave reads every (m, l) and accumulator in one round trip.  Beyond that, two
 // dependent round trips: every slot's (m, l) is staged in LDS at once, then the
 // accumulators of the non-empty slots are read with many loads in flight.
+// n_slots: the items per (b, h) of a fixed-count launch; for a balanced launch
+// (p.part_n set) each row's count is read from p.part_n and n_slots is the number
+// of slots loaded before it arrives (at most kMergeFastSlots and max_items); rows
+// of one item are skipped (the finalize wrote their output).
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
   __shared__ float m_lds[kMaxMergeSlots][G];
@@ -1007,43 +1084,67 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   const int b = bh / p.n_kv_heads;
   const int h = bh - b * p.n_kv_heads;
   const int n_rep = p.rep_ml ? p.n_rc : 0;
-  const int n_all = min(n_slots + n_rep, kMaxMergeSlots);
+  // counted (balanced) launches: the row's item count comes from the finalize, and
+  // wave 0 loads the first n_slots slots while it is in flight
+  const bool counted = p.part_n != nullptr;
+  constexpr int PER = G * D / 64;  // outputs per lane of one wave (all in query row o0 / D)
+  const int o0 = lane * PER;
+  const int g0 = o0 / D;
+  float mv[kMergeFastSlots], lv[kMergeFastSlots], av[kMergeFastSlots][PER];
+  auto load_slot = [&](int s, const float* ml, const float* src) {
+    mv[s] = ml[g0 * 2];
+    lv[s] = ml[g0 * 2 + 1];
+    if constexpr (PER % 4 == 0) {
+#pragma unroll
+      for (int e = 0; e < PER; e += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(src + o0 + e);
+        av[s][e] = w4.x; av[s][e + 1] = w4.y; av[s][e + 2] = w4.z; av[s][e + 3] = w4.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) av[s][e] = src[o0 + e];
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < kMergeFastSlots; ++s) {
+    mv[s] = kNegInf;
+    lv[s] = 0.f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
+  }
+  int n_fin = n_slots;
+  if (counted) {
+    n_fin = min(max(p.part_n[bh], 0), p.max_items);
+    if (wave == 0) {
+#pragma unroll
+      for (int s = 0; s < kMergeFastSlots; ++s) {
+        const int64_t slot = (int64_t)bh * p.max_items + s;
+        if (s < n_slots) load_slot(s, p.part_ml + slot * G * 2, p.part_acc + slot * (G * D));
+      }
+    }
+    if (n_fin <= 1) return;  // a row of one item: the finalize wrote its output
+  }
+  const int n_all = min(n_fin + n_rep, kMaxMergeSlots);
   auto ml_of = [&](int s) -> const float* {
-    return s < n_slots ? p.part_ml + ((int64_t)bh * p.max_items + s) * G * 2
-                       : p.rep_ml + ((int64_t)bh * p.n_rc + (s - n_slots)) * G * 2;
+    return s < n_fin ? p.part_ml + ((int64_t)bh * p.max_items + s) * G * 2
+                     : p.rep_ml + ((int64_t)bh * p.n_rc + (s - n_fin)) * G * 2;
   };
   auto acc_of = [&](int s) -> const float* {
-    return s < n_slots ? p.part_acc + ((int64_t)bh * p.max_items + s) * (G * D)
-                       : p.rep_acc + ((int64_t)bh * p.n_rc + (s - n_slots)) * (G * D);
+    return s < n_fin ? p.part_acc + ((int64_t)bh * p.max_items + s) * (G * D)
+                     : p.rep_acc + ((int64_t)bh * p.n_rc + (s - n_fin)) * (G * D);
   };
-  constexpr int PER = G * D / 64;  // outputs per lane of one wave (all in query row o0 / D)
   if (n_all <= kMergeFastSlots) {
     // few slots: wave 0 loads every slot's (m, l) and accumulators in one round trip
     if (wave != 0) return;
-    const int o0 = lane * PER;
-    const int g0 = o0 / D;
-    float mv[kMergeFastSlots], lv[kMergeFastSlots], av[kMergeFastSlots][PER];
+    const int s_have = counted ? n_slots : 0;
 #pragma unroll
     for (int s = 0; s < kMergeFastSlots; ++s) {
-      mv[s] = kNegInf;
-      lv[s] = 0.f;
+      if (s >= s_have && s < n_all) load_slot(s, ml_of(s), acc_of(s));
+      if (s >= n_all) {  // speculative loads past the row's items
+        mv[s] = kNegInf;
+        lv[s] = 0.f;
 #pragma unroll
-      for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
-      if (s < n_all) {
-        const float* ml = ml_of(s) + g0 * 2;
-        mv[s] = ml[0];
-        lv[s] = ml[1];
-        const float* src = acc_of(s) + o0;
-        if constexpr (PER % 4 == 0) {
-#pragma unroll
-          for (int e = 0; e < PER; e += 4) {
-            const float4 w4 = *reinterpret_cast<const float4*>(src + e);
-            av[s][e] = w4.x; av[s][e + 1] = w4.y; av[s][e + 2] = w4.z; av[s][e + 3] = w4.w;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < PER; ++e) av[s][e] = src[e];
-        }
+        for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
       }
     }
     float M = kNegInf;
@@ -1106,8 +1207,6 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   // outputs of the slot's [G, D] block (vector loads), kU slots in flight
   constexpr int kU = 4;
   const int nl = n_list;
-  const int o0 = lane * PER;
-  const int g0 = o0 / D;
   float a[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) a[e] = 0.f;
@@ -1157,9 +1256,17 @@ template <int D, int G, typename KV, int SRC>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kFinThreads), 0, st, p);
   int rc = check_launch("paged decode");
-  if (rc || (grid.x == 1 && !p.rep_ml)) return rc;
-  hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(grid.y * grid.z), dim3(kThreads), 0, st, p,
-                     (int)grid.x);
+  if constexpr (src_balanced(SRC)) {
+    // a flat grid of at most n_rows workgroups gives every row a single item
+    if (rc || (int)grid.x <= p.n_rows) return rc;
+    const int even = ((int)grid.x + p.n_rows - 1) / p.n_rows;
+    const int spec = std::min(kMergeFastSlots, std::min(p.max_items, even));
+    hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(p.n_rows), dim3(kThreads), 0, st, p, spec);
+  } else {
+    if (rc || (grid.x == 1 && !p.rep_ml)) return rc;
+    hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(grid.y * grid.z), dim3(kThreads), 0, st, p,
+                       (int)grid.x);
+  }
   return check_launch("split-k merge");
 }
 
@@ -1183,6 +1290,9 @@ int resident_wgs() {
 // Host helpers shared by the decode entry points (paged_decode.hip).
 int units_cap_items(int64_t units);
 size_t decode_ws_size(int batch, int hkv, int group, int d, int max_items);
+void set_decode_ws(DecodeParams& p, char* ws, int64_t bh, int max_items, int group, int d);
+int balanced_grid(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t n_rows, int64_t units_max,
+                  int nsub_u, int cap_items, hipStream_t st, int* grid_out, int* budget_out);
 int check_kv(const ia_paged_kv* kv, int d);
 int check_shape(const ia_decode_shape* s);
 int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, dim3 grid, hipStream_t st,
@@ -1190,10 +1300,10 @@ int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, 
 int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
                  int nsub_u, int cap_items, hipStream_t st, int* items_out);
 
-// Block scores of the fused top-k decode (select_topk.hip).
+// Block scores of the fused top-k decode and its finalize's launch plan (select_topk.hip).
 int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
                     int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
-                    int32_t nb_max, float* scores, hipStream_t st);
+                    int32_t nb_max, float* scores, const TopkPlanArgs& plan, hipStream_t st);
 
 // Dispatch by kv dtype for one (D, G): defined in paged_decode_{bf16,f32,fp8}.hip.
 int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
@@ -1201,3 +1311,4 @@ int dispatch_f32(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStr
 int dispatch_fp8(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
 
 }  // namespace ia
+

@@ -18,6 +18,7 @@
 //       block ids in ascending order.
 //   The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
 //   with the mean key (k_bar) as the block representative.
+#include "plan.hpp"
 #include "topk_select.hpp"
 
 namespace ia {
@@ -43,6 +44,10 @@ struct SelectParams {
   int32_t n_kv_heads;
   float score_scale;   // 1 / (G * sqrt(D))
   int32_t lds_scores;  // score rows of up to this many blocks stay in LDS
+  // fused top-k decode: the finalize launch's plan, written by workgroup x = 0 of the
+  // scorer launch (one entry per finalize workgroup)
+  PlanEntry* plan;
+  int32_t plan_grid, plan_budget, plan_max_items, n_rows;
 };
 
 template <int D, int G, bool QF32, bool KBF16>
@@ -142,14 +147,61 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
 }
 
 // Scores of every block for the fused top-k decode (the selection itself runs in
-// the finalize's prologue): grid (ceil(nb_max / kScoreBlocksPerWg), Hkv, batch),
-// 256 threads; wave w scores blocks kScoreBlocksPerWg*blockIdx.x + 4*(kScoreRows*w + t) + r,
-// t < kScoreRows, every row of a lane in flight at once.  Same arithmetic as the
-// selector's scoring (bit-identical scores); -inf past the sequence's end.
+// the finalize's prologue): grid (1 + ceil(nb_max / kScoreBlocksPerWg), Hkv, batch),
+// 256 threads; workgroup (0, 0, 0) writes the finalize's launch plan, the others of
+// slice x = 0 exit; in slice x = 1 + bx, wave w scores blocks
+// kScoreBlocksPerWg*bx + 4*(kScoreRows*w + t) + r, t < kScoreRows, every row of a lane
+// in flight at once.  Same arithmetic as the selector's scoring (bit-identical
+// scores); -inf past the sequence's end.
 constexpr int kScoreRows = 4;                         // k_bar rows per lane
 constexpr int kScoreBlocksPerWg = 4 * 4 * kScoreRows;  // 4 waves x 4 rows per load x kScoreRows
+
+// The fused finalize's launch plan (plan.hpp), by one wave: the rows' units are the
+// counts of the top-k rule (the finalize selects exactly that many blocks).
+__device__ void write_fused_plan(const SelectParams& p) {
+  const int lane = threadIdx.x & 63;
+  const int nsub_u = p.block_size / 16;
+  auto units_of = [&](int r, int& len, int& k_row) -> int {
+    const int b = r / p.n_kv_heads;
+    len = max(p.seq_lens[b], 0);
+    k_row = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.k;
+    const int nbs = min(cdiv_pos(len, p.block_size), p.nb_max);
+    return topk_count(nbs, TopkRule{p.forced_first, p.forced_last, k_row, p.forced_in_k, p.k_cap});
+  };
+  auto slots_of = [&](int r) -> int {
+    int len, k_row;
+    return units_of(r, len, k_row) * nsub_u;
+  };
+  PlanRows rows;
+  const int t = plan_t_wave(slots_of, p.n_rows, p.plan_budget, p.plan_max_items, nsub_u, rows);
+  const int used = plan_walk_wave(slots_of, rows, p.n_rows, t, [&](bool active, int r, int s, int n, int first) {
+    if (active) {
+      int len, k_row;
+      units_of(r, len, k_row);
+      for (int i = 0; i < n; ++i) {
+        PlanEntry e;
+        plan_fill(e, r, s, n, i, nsub_u);
+        e.seq_len = len;
+        e.k_row = k_row;
+        p.plan[first + i] = e;
+      }
+    }
+    return false;
+  });
+  for (int w = used + lane; w < p.plan_grid; w += 64) {
+    PlanEntry e{};
+    e.row = -1;
+    p.plan[w] = e;
+  }
+}
+
 template <int D, int G, bool QF32, bool KBF16>
 __global__ __launch_bounds__(256) void ia_condition_block_topk_scores(SelectParams p) {
+  if (blockIdx.x == 0) {  // the plan slice: one wave of one workgroup
+    if (blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 64) write_fused_plan(p);
+    return;
+  }
+  const int bx = blockIdx.x - 1;
   constexpr int DPL = D / 16;
   constexpr int EB = KBF16 ? 2 : 4;
   constexpr int NWR = DPL * EB / 4;
@@ -160,7 +212,7 @@ __global__ __launch_bounds__(256) void ia_condition_block_topk_scores(SelectPara
   const int h = blockIdx.y;
   const int b = blockIdx.z;
   const int bh = b * p.n_kv_heads + h;
-  const int j0 = kScoreBlocksPerWg * blockIdx.x + 4 * kScoreRows * wave;
+  const int j0 = kScoreBlocksPerWg * bx + 4 * kScoreRows * wave;
   if (j0 >= p.nb_max) return;  // whole wave
   const int seq_len = max(p.seq_lens[b], 0);
   const int nb = min((seq_len + p.block_size - 1) / p.block_size, p.nb_max);
@@ -243,7 +295,7 @@ int launch_select(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipSt
 
 int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
                     int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
-                    int32_t nb_max, float* scores, hipStream_t st) {
+                    int32_t nb_max, float* scores, const TopkPlanArgs& plan, hipStream_t st) {
   const int G = shape->n_q_heads / shape->n_kv_heads;
   const int D = shape->head_dim;
   SelectParams p{};
@@ -259,7 +311,18 @@ int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_b
   p.scores = scores;
   p.n_kv_heads = shape->n_kv_heads;
   p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
-  const dim3 grid((nb_max + kScoreBlocksPerWg - 1) / kScoreBlocksPerWg, shape->n_kv_heads, shape->batch);
+  p.k = plan.k;
+  p.k_per_seq = plan.k_per_seq;
+  p.forced_first = plan.forced_first;
+  p.forced_last = plan.forced_last;
+  p.forced_in_k = plan.forced_in_k;
+  p.k_cap = plan.k_cap;
+  p.plan = plan.entries;
+  p.plan_grid = plan.grid;
+  p.plan_budget = plan.budget;
+  p.plan_max_items = plan.max_items;
+  p.n_rows = plan.n_rows;
+  const dim3 grid(1 + (nb_max + kScoreBlocksPerWg - 1) / kScoreBlocksPerWg, shape->n_kv_heads, shape->batch);
   const bool qf32 = shape->q_dtype == IA_F32;
   const bool kbf16 = k_bar_dtype == IA_BF16;
 #define IA_SC(DD, GG) \

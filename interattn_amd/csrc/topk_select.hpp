@@ -147,6 +147,31 @@ struct TopkForced {
   __device__ bool operator()(int j) const { return j < ff || j >= fl_start; }
 };
 
+// Sizes the rule fixes before any score is read: forced blocks, candidates and
+// the number of candidates taken (k_eff).
+struct TopkSizes {
+  int ff, fl_start, n_forced, n_cand, k_eff;
+};
+__device__ __forceinline__ TopkSizes topk_sizes(int nb, const TopkRule& rule) {
+  const TopkForced f(rule, nb);
+  TopkSizes z;
+  z.ff = f.ff;
+  z.fl_start = f.fl_start;
+  z.n_forced = f.ff + (nb - max(f.fl_start, f.ff));  // |[0,ff) U [fl_start,nb)|
+  z.n_cand = nb - z.n_forced;
+  int k_eff = rule.forced_in_k ? rule.k - z.n_forced : rule.k;
+  k_eff = max(k_eff, 0);
+  z.k_eff = min(k_eff, max(rule.k_cap - z.n_forced, 0));
+  return z;
+}
+
+// Number of blocks topk_select chooses from a row of nb blocks (whatever the
+// scores): every forced block, min(k_eff, candidates) others, clamped to k_cap.
+__device__ __forceinline__ int topk_count(int nb, const TopkRule& rule) {
+  const TopkSizes z = topk_sizes(nb, rule);
+  return min(z.n_forced + min(z.k_eff, z.n_cand), rule.k_cap);
+}
+
 // Staged start of topk_select (for a caller that already walks the score row, e.g.
 // while copying it to LDS): each thread passes the largest key and the largest ~key
 // of the candidates it saw; the per-wave values land in L.red and the histogram is
@@ -174,13 +199,9 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
   constexpr int kWv = NT / 64;
   const int wave = threadIdx.x >> 6;
   const TopkForced is_forced(rule, nb);
-  const int ff = is_forced.ff;
-  const int fl_start = is_forced.fl_start;
-  const int n_forced = ff + (nb - max(fl_start, ff));  // |[0,ff) U [fl_start,nb)|
-  const int n_cand = nb - n_forced;
-  int k_eff = rule.forced_in_k ? rule.k - n_forced : rule.k;
-  k_eff = max(k_eff, 0);
-  k_eff = min(k_eff, max(rule.k_cap - n_forced, 0));
+  const TopkSizes sizes = topk_sizes(nb, rule);
+  const int n_cand = sizes.n_cand;
+  const int k_eff = sizes.k_eff;
   // consecutive indices per thread in the scans over the row (all threads busy)
   const int seg = min(kSegElems, max(1, (nb + NT - 1) / NT));
 

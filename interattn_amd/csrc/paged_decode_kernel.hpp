@@ -321,9 +321,56 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // sources; the fused top-k plan comes from the scorer launch), else from the grid
   int b, h, item, n_items_row = 1, slot_lo = 0, slot_hi = 0, seq_len = 0, n_units = 0, n_blk_units = 0, sfx_len = 0;
   int k_b = p.topk_k;
+
+  // query rows of kv head hq of sequence bq: raw loads, converted after the
+  // prologue.  Vector path: every row at the lane's dim slice c16*DPL ..; MFMA path:
+  // row c16 % G at the dims of the lane's k-slices.
+  constexpr int QR0 = kMfma ? kMfmaK : G;
+  constexpr int QR1 = kMfma ? 8 : DPL;
+  u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs (upper half unused)
+  auto load_q = [&](int bq, int hq) {
+#pragma unroll
+    for (int x = 0; x < QR0; ++x) {
+      const int g = kMfma ? c16 % G : x;
+      const int d0 = kMfma ? mfma_kslice<KV::kBytes>(x, r) : c16 * DPL;
+      constexpr int NE = kMfma ? 8 : DPL;
+      const int64_t row = (int64_t)bq * p.q_batch_stride + (int64_t)(hq * G + g) * p.q_row_stride;
+      if (p.q_f32) {
+        const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < NE; ++e) qraw[x][e] = qp[e];
+      } else {
+        const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
+#pragma unroll
+        for (int e = 0; e < NE / 2; ++e) qraw[x][e] = (u32)qp[2 * e] | ((u32)qp[2 * e + 1] << 16);
+#pragma unroll
+        for (int e = NE / 2; e < QR1; ++e) qraw[x][e] = 0u;
+      }
+    }
+  };
+  // fused top-k: the row's score row (-inf past its sequence, up to nb_max)
+  constexpr int kScPer = SRC == kSrcTopkFused ? kFusedMaxBlocks / kFinThreads : 1;
+  float scv[kScPer];
+  auto load_scores = [&](int row) {
+    const float* sr = p.scores + (int64_t)row * p.nb_max;
+#pragma unroll
+    for (int i = 0; i < kScPer; ++i) {
+      const int t = threadIdx.x + i * kFinThreads;
+      scv[i] = t < p.nb_max ? sr[t] : kNegInf;
+    }
+  };
+
+  int spec_row = -1;
   if constexpr (kBalanced) {
     PlanEntry e;
     if constexpr (SRC == kSrcTopkFused) {
+      // the plan entry, the query rows and the score row in one round trip: the
+      // last two for the row of an even split (the plan's row whenever every row has
+      // the same work), fetched again after the entry on a miss
+      spec_row = (int)(((long long)blockIdx.x * p.n_rows) / gridDim.x);
+      const int sb = spec_row / p.n_kv_heads;
+      load_q(sb, spec_row - sb * p.n_kv_heads);
+      load_scores(spec_row);
       e = p.plan[blockIdx.x];
     } else {
       if (wave == 0) {
@@ -348,6 +395,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     if constexpr (SRC == kSrcTopkFused) {
       seq_len = __builtin_amdgcn_readfirstlane(e.seq_len);
       k_b = __builtin_amdgcn_readfirstlane(e.k_row);
+      if (row != spec_row) load_scores(row);
     } else {
       seq_len = max(p.seq_lens[b], 0);
     }
@@ -357,48 +405,27 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     item = blockIdx.x;
   }
   const int bh = b * p.n_kv_heads + h;
-
-  // ---- query rows of this kv head: raw loads issued first (independent of the
-  // rest of the prologue), converted after it.  Vector path: every row at the lane's
-  // dim slice c16*DPL ..; MFMA path: row c16 % G at the dims of the lane's k-slices.
-  constexpr int QR0 = kMfma ? kMfmaK : G;
-  constexpr int QR1 = kMfma ? 8 : DPL;
-  u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs (upper half unused)
-#pragma unroll
-  for (int x = 0; x < QR0; ++x) {
-    const int g = kMfma ? c16 % G : x;
-    const int d0 = kMfma ? mfma_kslice<KV::kBytes>(x, r) : c16 * DPL;
-    constexpr int NE = kMfma ? 8 : DPL;
-    const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride;
-    if (p.q_f32) {
-      const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
-#pragma unroll
-      for (int e = 0; e < NE; ++e) qraw[x][e] = qp[e];
-    } else {
-      const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + row + d0;
-#pragma unroll
-      for (int e = 0; e < NE / 2; ++e) qraw[x][e] = (u32)qp[2 * e] | ((u32)qp[2 * e + 1] << 16);
-#pragma unroll
-      for (int e = NE / 2; e < QR1; ++e) qraw[x][e] = 0u;
-    }
-  }
+  if (bh != spec_row) load_q(b, h);
 
   if constexpr (SRC == kSrcTopkFused) {
     // the whole score row in LDS, then the shared top-k rule (every item of the row
     // selects the same blocks; item 0 publishes them)
     const int nbs = min(cdiv_pos(seq_len, p.unit_tokens), p.nb_max);
-    const float* sc_row = p.scores + (int64_t)bh * p.nb_max;
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
     // staging the row also gives the selection its candidates' key range
     const TopkForced forced(rule, nbs);
     u32 kmx = 0u, kmn_inv = 0u;
-    for (int t = threadIdx.x; t < nbs; t += kFinThreads) {
-      const float v = sc_row[t];
-      fsc[t] = v;
-      if (!forced(t)) {
-        const u32 key = order_key(v);
-        kmx = max(kmx, key);
-        kmn_inv = max(kmn_inv, ~key);
+#pragma unroll
+    for (int i = 0; i < kScPer; ++i) {
+      const int t = threadIdx.x + i * kFinThreads;
+      if (t < nbs) {
+        const float v = scv[i];
+        fsc[t] = v;
+        if (!forced(t)) {
+          const u32 key = order_key(v);
+          kmx = max(kmx, key);
+          kmn_inv = max(kmn_inv, ~key);
+        }
       }
     }
     topk_stage<kFinThreads>(ftk, kmx, kmn_inv);

@@ -376,8 +376,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       if (wave == 0) {
         PlanRows rows;
         auto slots_of = [&](int rr) -> int { return plan_row_units<SRC>(p, rr) * nsub_u; };
-        const int t = plan_t_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
-        const PlanEntry pe = plan_entry_wave(slots_of, rows, p.n_rows, t, (int)blockIdx.x, nsub_u);
+        const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
+        const PlanEntry pe = plan_entry_wave(slots_of, rows, p.n_rows, rule, (int)blockIdx.x, nsub_u);
         if (lane == 0) plan_lds = pe;
       }
       __syncthreads();
@@ -1086,18 +1086,19 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
 }
 
 constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
-constexpr int kMergeFastSlots = 8;  // up to this many slots: one round trip, one wave
+constexpr int kMergeFastSlots = 8;  // slots per wave read in the merge's one-round-trip path
 
 // Split-K merge, one workgroup per (sequence, kv head): out = sum_s f_s acc_s / sum_s f_s l_s
 // with f_s = 2^(m_s - M) over the finalize items' partials and the route chunks'
-// representative partials (CBT/legacy.py:765-794).  Up to kMergeFastSlots slots
-// one wave reads every (m, l) and accumulator in one round trip.  Beyond that, two
+// representative partials (CBT/legacy.py:765-794).  Up to kWaves x kMergeFastSlots
+// slots are read in one round trip (one wave up to kMergeFastSlots, else every wave
+// its eight, folded in LDS).  Beyond that, two
 // dependent round trips: every slot's (m, l) is staged in LDS at once, then the
 // accumulators of the non-empty slots are read with many loads in flight.
 // n_slots: the items per (b, h) of a fixed-count launch; for a balanced launch
 // (p.part_n set) each row's count is read from p.part_n and n_slots is the number
-// of slots loaded before it arrives (at most kMergeFastSlots and max_items); rows
-// of one item are skipped (the finalize wrote their output).
+// of slots loaded before it arrives (at most kWaves x kMergeFastSlots and max_items);
+// rows of one item are skipped (the finalize wrote their output).
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(DecodeParams p, int n_slots) {
   __shared__ float m_lds[kMaxMergeSlots][G];
@@ -1117,37 +1118,38 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   constexpr int PER = G * D / 64;  // outputs per lane of one wave (all in query row o0 / D)
   const int o0 = lane * PER;
   const int g0 = o0 / D;
+  // wave w holds slots 8 w .. 8 w + 7: up to kWaves * 8 slots in one round trip
   float mv[kMergeFastSlots], lv[kMergeFastSlots], av[kMergeFastSlots][PER];
-  auto load_slot = [&](int s, const float* ml, const float* src) {
-    mv[s] = ml[g0 * 2];
-    lv[s] = ml[g0 * 2 + 1];
+  auto load_slot = [&](int j, const float* ml, const float* src) {
+    mv[j] = ml[g0 * 2];
+    lv[j] = ml[g0 * 2 + 1];
     if constexpr (PER % 4 == 0) {
 #pragma unroll
       for (int e = 0; e < PER; e += 4) {
         const float4 w4 = *reinterpret_cast<const float4*>(src + o0 + e);
-        av[s][e] = w4.x; av[s][e + 1] = w4.y; av[s][e + 2] = w4.z; av[s][e + 3] = w4.w;
+        av[j][e] = w4.x; av[j][e + 1] = w4.y; av[j][e + 2] = w4.z; av[j][e + 3] = w4.w;
       }
     } else {
 #pragma unroll
-      for (int e = 0; e < PER; ++e) av[s][e] = src[o0 + e];
+      for (int e = 0; e < PER; ++e) av[j][e] = src[o0 + e];
     }
   };
+  auto clear_slot = [&](int j) {
+    mv[j] = kNegInf;
+    lv[j] = 0.f;
 #pragma unroll
-  for (int s = 0; s < kMergeFastSlots; ++s) {
-    mv[s] = kNegInf;
-    lv[s] = 0.f;
+    for (int e = 0; e < PER; ++e) av[j][e] = 0.f;
+  };
 #pragma unroll
-    for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
-  }
+  for (int j = 0; j < kMergeFastSlots; ++j) clear_slot(j);
   int n_fin = n_slots;
   if (counted) {
     n_fin = min(max(p.part_n[bh], 0), p.max_items);
-    if (wave == 0) {
 #pragma unroll
-      for (int s = 0; s < kMergeFastSlots; ++s) {
-        const int64_t slot = (int64_t)bh * p.max_items + s;
-        if (s < n_slots) load_slot(s, p.part_ml + slot * G * 2, p.part_acc + slot * (G * D));
-      }
+    for (int j = 0; j < kMergeFastSlots; ++j) {
+      const int s = kMergeFastSlots * wave + j;
+      const int64_t slot = (int64_t)bh * p.max_items + s;
+      if (s < n_slots) load_slot(j, p.part_ml + slot * G * 2, p.part_acc + slot * (G * D));
     }
     if (n_fin <= 1) return;  // a row of one item: the finalize wrote its output
   }
@@ -1160,32 +1162,59 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
     return s < n_fin ? p.part_acc + ((int64_t)bh * p.max_items + s) * (G * D)
                      : p.rep_acc + ((int64_t)bh * p.n_rc + (s - n_fin)) * (G * D);
   };
-  if (n_all <= kMergeFastSlots) {
-    // few slots: wave 0 loads every slot's (m, l) and accumulators in one round trip
-    if (wave != 0) return;
+  if (n_all <= kWaves * kMergeFastSlots) {
+    // few slots: every slot's (m, l) and accumulators in one round trip (wave 0
+    // alone up to 8 slots, else four waves folded in LDS)
+    const bool solo = n_all <= kMergeFastSlots;
+    if (solo && wave != 0) return;
     const int s_have = counted ? n_slots : 0;
 #pragma unroll
-    for (int s = 0; s < kMergeFastSlots; ++s) {
-      if (s >= s_have && s < n_all) load_slot(s, ml_of(s), acc_of(s));
-      if (s >= n_all) {  // speculative loads past the row's items
-        mv[s] = kNegInf;
-        lv[s] = 0.f;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) av[s][e] = 0.f;
-      }
+    for (int j = 0; j < kMergeFastSlots; ++j) {
+      const int s = kMergeFastSlots * wave + j;
+      if (s >= s_have && s < n_all) load_slot(j, ml_of(s), acc_of(s));
+      if (s >= n_all) clear_slot(j);  // speculative loads past the row's items
     }
     float M = kNegInf;
 #pragma unroll
-    for (int s = 0; s < kMergeFastSlots; ++s) M = fmaxf(M, mv[s]);
+    for (int j = 0; j < kMergeFastSlots; ++j) M = fmaxf(M, mv[j]);
     float L = 0.f, a[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) a[e] = 0.f;
+    if (M != kNegInf) {
 #pragma unroll
-    for (int s = 0; s < kMergeFastSlots; ++s) {
-      const float f = (mv[s] == kNegInf) ? 0.f : exp2f(mv[s] - M);
-      L += f * lv[s];
+      for (int j = 0; j < kMergeFastSlots; ++j) {
+        const float f = (mv[j] == kNegInf) ? 0.f : exp2f(mv[j] - M);
+        L += f * lv[j];
 #pragma unroll
-      for (int e = 0; e < PER; ++e) a[e] = fmaf(f, av[s][e], a[e]);
+        for (int e = 0; e < PER; ++e) a[e] = fmaf(f, av[j][e], a[e]);
+      }
+    }
+    if (!solo) {
+      __shared__ float wm_f[kWaves][64];
+      __shared__ float wl_f[kWaves][64];
+      __shared__ float wa_f[kWaves][G * D];
+      wm_f[wave][lane] = M;
+      wl_f[wave][lane] = L;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) wa_f[wave][o0 + e] = a[e];
+      __syncthreads();
+      if (wave != 0) return;
+      M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, wm_f[w][lane]);
+      L = 0.f;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) a[e] = 0.f;
+      if (M != kNegInf) {
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float mw = wm_f[w][lane];
+          const float f = (mw == kNegInf) ? 0.f : exp2f(mw - M);
+          L += f * wl_f[w][lane];
+#pragma unroll
+          for (int e = 0; e < PER; ++e) a[e] = fmaf(f, wa_f[w][o0 + e], a[e]);
+        }
+      }
     }
 #pragma unroll
     for (int e = 0; e < PER; ++e) store_decode_out<G, D>(p, b, h, o0 + e, a[e] / fmaxf(L, 1e-30f));
@@ -1287,7 +1316,7 @@ int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
     // a flat grid of at most n_rows workgroups gives every row a single item
     if (rc || (int)grid.x <= p.n_rows) return rc;
     const int even = ((int)grid.x + p.n_rows - 1) / p.n_rows;
-    const int spec = std::min(kMergeFastSlots, std::min(p.max_items, even));
+    const int spec = std::min(kWaves * kMergeFastSlots, std::min(p.max_items, even));
     hipLaunchKernelGGL((ia_condition_block_splitk_merge<D, G>), dim3(p.n_rows), dim3(kThreads), 0, st, p, spec);
   } else {
     if (rc || (grid.x == 1 && !p.rep_ml)) return rc;

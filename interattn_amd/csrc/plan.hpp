@@ -2,19 +2,23 @@
 //
 // A balanced launch is one flat grid of workgroups over the (sequence, kv head)
 // rows, r = b * Hkv + h.  With S_r = the row's units x subtiles per unit ("raw
-// slots", unit-major), the plan takes t = the smallest per-item slot budget in
-// [t_lo, t_hi] with
-//     sum_r max(1, ceil(S_r / t)) <= budget            (budget = resident workgroups)
-// (or t_hi when none fits); row r gets n_r = max(1, ceil(S_r / t)) items, item i the
-// slots [i q_r, min((i + 1) q_r, S_r)) with q_r = ceil(S_r / n_r) (never empty when
-// S_r > 0); items are numbered row by row over the grid and the workgroups past the
-// last item are idle.  t_lo keeps n_r <= max_items (the partial stride) and items of
-// at least one unit; t_hi keeps an item's unit ranges and subtile list within the
-// finalize's LDS arrays.  Every function here runs in one wave, without barriers:
-// the fused top-k launch computes the plan once, in a workgroup of the scorer
-// launch, and each finalize workgroup reads its entry; the other launches compute it
-// in one wave of each finalize workgroup.  Both evaluate the same code on the same
-// S_r, so they agree bit for bit.
+// slots", unit-major), row r gets n_r items:
+//   * every row alike (S_r = S): n = budget / rows items per row (budget = resident
+//     workgroups), so the grid is used whole and workgroup w serves row
+//     w / (grid / rows) (the guess the fused finalize loads ahead with); clamped to
+//     at most max_items (the partial stride) and S / units-per-slot (items of at
+//     least one unit), and to at least ceil(S / t_hi);
+//   * otherwise n_r = max(1, ceil(S_r / t)) with t the smallest per-item slot budget
+//     in [t_lo, t_hi] such that sum_r n_r <= budget (t_hi when none fits).  t_lo keeps
+//     n_r <= max_items and items of at least one unit.
+// Item i of a row covers q + 1 slots for i < rem and q slots after, q = S / n and
+// rem = S - q n (never empty when S >= n); items are numbered row by row
+// over the grid and the workgroups past the last item are idle.  t_hi keeps an
+// item's unit ranges and subtile list within the finalize's LDS arrays.  Every
+// function here runs in one wave, without barriers: the fused top-k launch computes
+// the plan once, in a workgroup of the scorer launch, and each finalize workgroup
+// reads its entry; the other launches compute it in one wave of each finalize
+// workgroup.  Both evaluate the same code on the same S_r, so they agree bit for bit.
 #pragma once
 
 #include "topk_select.hpp"
@@ -74,10 +78,17 @@ struct PlanRows {
   int s[kPlanRegRows];
 };
 
-// t of the plan, computed by one wave (every lane returns it).  slots_of(r) gives S_r
-// for any row (rows past the register stage are read through it again).
+// The rule that sets each row's item count (see the top of this file).
+struct PlanRule {
+  int t;      // per-item slot budget (rows of unequal work)
+  int n_all;  // items of every row when all rows have the same work, else 0
+};
+
+// The plan's rule, computed by one wave (every lane returns it).  slots_of(r) gives
+// S_r for any row (rows past the register stage are read through it again).
 template <typename SlotsOf>
-__device__ int plan_t_wave(SlotsOf slots_of, int nrows, int budget, int max_items, int nsub_u, PlanRows& rows) {
+__device__ PlanRule plan_rule_wave(SlotsOf slots_of, int nrows, int budget, int max_items, int nsub_u,
+                                   PlanRows& rows) {
   const int lane = threadIdx.x & 63;
   int ssum = 0, smax = 0;
 #pragma unroll
@@ -95,16 +106,19 @@ __device__ int plan_t_wave(SlotsOf slots_of, int nrows, int budget, int max_item
   ssum = wave_sum_i(ssum);
   smax = (int)wave_u32_max((u32)smax);
   budget = max(budget, nrows);
+  max_items = max(max_items, 1);
   const int t_cap = plan_t_cap(nsub_u);
-  const int t_floor = min(max(nsub_u, cdiv_pos(smax, max(max_items, 1))), t_cap);
+  if ((int64_t)smax * nrows == (int64_t)ssum) {
+    // every row alike: budget / rows items per row
+    int n = min(budget / nrows, min(max_items, max(smax / nsub_u, 1)));
+    n = max(n, max(cdiv_pos(smax, t_cap), 1));
+    return PlanRule{0, n};
+  }
+  const int t_floor = min(max(nsub_u, cdiv_pos(smax, max_items)), t_cap);
   int lo = min(max(t_floor, cdiv_pos(ssum, budget)), t_cap);
   int hi = max(lo, min(smax, t_cap));
   // sum_r max(1, ceil(S_r / t)) <= ssum / t + nrows: this t always fits the budget
   if (budget > nrows) hi = max(lo, min(hi, cdiv_pos(ssum, budget - nrows)));
-  if ((int64_t)smax * nrows == (int64_t)ssum) {
-    // every row alike: nrows * ceil(S / t) <= budget iff t >= ceil(S / (budget / nrows))
-    return smax == 0 ? lo : min(max(lo, cdiv_pos(smax, budget / nrows)), hi);
-  }
   auto items_at = [&](int t) -> int {
     const float rt = __builtin_amdgcn_rcpf((float)t);
     int a = 0;
@@ -119,7 +133,7 @@ __device__ int plan_t_wave(SlotsOf slots_of, int nrows, int budget, int max_item
     if (items_at(mid) <= budget) hi = mid;
     else lo = mid + 1;
   }
-  return lo;
+  return PlanRule{lo, 0};
 }
 
 // Visit every row's items in grid order: visit(lane_active, r, S_r, n_r, first item's
@@ -127,9 +141,9 @@ __device__ int plan_t_wave(SlotsOf slots_of, int nrows, int budget, int max_item
 // nrows) and ends the walk by returning true (a uniform value); returns the number of
 // workgroups the visited rows' items take.
 template <typename SlotsOf, typename Visit>
-__device__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, int t, Visit visit) {
+__device__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, Visit visit) {
   const int lane = threadIdx.x & 63;
-  const float rt = __builtin_amdgcn_rcpf((float)t);
+  const float rt = __builtin_amdgcn_rcpf((float)max(rule.t, 1));
   int base = 0;
   for (int r0 = 0; r0 < nrows; r0 += 64) {
     const int r = r0 + lane;
@@ -144,7 +158,7 @@ __device__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows,
         s = slots_of(r);
       }
     }
-    const int n = r < nrows ? max(1, ceil_div_rcp(s, t, rt)) : 0;
+    const int n = r >= nrows ? 0 : rule.n_all > 0 ? rule.n_all : max(1, ceil_div_rcp(s, rule.t, rt));
     const int inc = wave_inclusive_scan(n);
     if (visit(r < nrows, r, s, n, base + inc - n)) return base;  // uniform stop
     base += __builtin_amdgcn_readlane(inc, 63);
@@ -152,24 +166,34 @@ __device__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows,
   return base;
 }
 
-// Fill the entry of an item: row r with S_r = s slots in n items, item i.
-__device__ __forceinline__ void plan_fill(PlanEntry& e, int r, int s, int n, int i, int nsub_u) {
-  const int q = cdiv_pos(s, n);
-  e.row = r;
+// Row r's split: S_r = s slots in n items, q = s / n slots each and one more for the
+// first rem = s - q n items.
+struct PlanSplit {
+  int r, s, n, q, rem, n_units;
+};
+__device__ __forceinline__ PlanSplit plan_split(int r, int s, int n, int nsub_u) {
+  const int q = s / n;
+  return PlanSplit{r, s, n, q, s - q * n, s / nsub_u};
+}
+
+// Fill the entry of item i of a split (no division: called once per workgroup).
+__device__ __forceinline__ void plan_fill(PlanEntry& e, const PlanSplit& sp, int i) {
+  e.row = sp.r;
   e.item = i;
-  e.n_items = n;
-  e.slot_lo = i * q;
-  e.slot_hi = min(s, e.slot_lo + q);
-  e.n_units = s / nsub_u;
+  e.n_items = sp.n;
+  e.slot_lo = i * sp.q + min(i, sp.rem);
+  e.slot_hi = e.slot_lo + sp.q + (i < sp.rem ? 1 : 0);
+  e.n_units = sp.n_units;
 }
 
 // The entry of workgroup w (one wave; every lane returns it; row -1 when idle).
 // seq_len and k_row are left to the caller.
 template <typename SlotsOf>
-__device__ PlanEntry plan_entry_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, int t, int w, int nsub_u) {
+__device__ PlanEntry plan_entry_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, int w,
+                                     int nsub_u) {
   PlanEntry e{};
   e.row = -1;
-  plan_walk_wave(slots_of, rows, nrows, t, [&](bool active, int r, int s, int n, int first) -> bool {
+  plan_walk_wave(slots_of, rows, nrows, rule, [&](bool active, int r, int s, int n, int first) -> bool {
     const bool mine = active && w >= first && w < first + n;
     const unsigned long long bal = __ballot(mine);
     if (bal) {
@@ -178,7 +202,7 @@ __device__ PlanEntry plan_entry_wave(SlotsOf slots_of, const PlanRows& rows, int
       const int ss = __builtin_amdgcn_readlane(s, src);
       const int nn = __builtin_amdgcn_readlane(n, src);
       const int ff = __builtin_amdgcn_readlane(first, src);
-      plan_fill(e, rr, ss, nn, w - ff, nsub_u);
+      plan_fill(e, plan_split(rr, ss, nn, nsub_u), w - ff);
       return true;
     }
     return false;

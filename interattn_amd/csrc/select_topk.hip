@@ -173,14 +173,35 @@ __device__ void write_fused_plan(const SelectParams& p) {
     return units_of(r, len, k_row) * nsub_u;
   };
   PlanRows rows;
-  const int t = plan_t_wave(slots_of, p.n_rows, p.plan_budget, p.plan_max_items, nsub_u, rows);
-  const int used = plan_walk_wave(slots_of, rows, p.n_rows, t, [&](bool active, int r, int s, int n, int first) {
+  const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.plan_max_items, nsub_u, rows);
+  if (rule.n_all > 0) {
+    // every row alike: lane-strided over the grid's workgroups, row w / n_all
+    const int s = __builtin_amdgcn_readfirstlane(rows.s[0]);  // row 0 (lane 0): every row's S
+    const int n = rule.n_all;
+    const int used = p.n_rows * n;
+    for (int w = lane; w < p.plan_grid; w += 64) {
+      PlanEntry e{};
+      e.row = -1;
+      if (w < used) {
+        const int r = w / n;
+        int len, k_row;
+        units_of(r, len, k_row);
+        plan_fill(e, plan_split(r, s, n, nsub_u), w - r * n);
+        e.seq_len = len;
+        e.k_row = k_row;
+      }
+      p.plan[w] = e;
+    }
+    return;
+  }
+  const int used = plan_walk_wave(slots_of, rows, p.n_rows, rule, [&](bool active, int r, int s, int n, int first) {
     if (active) {
       int len, k_row;
       units_of(r, len, k_row);
+      const PlanSplit sp = plan_split(r, s, n, nsub_u);
       for (int i = 0; i < n; ++i) {
         PlanEntry e;
-        plan_fill(e, r, s, n, i, nsub_u);
+        plan_fill(e, sp, i);
         e.seq_len = len;
         e.k_row = k_row;
         p.plan[first + i] = e;

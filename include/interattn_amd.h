@@ -183,10 +183,12 @@ IA_API int ia_topk_block_mask(const int32_t* idx, const int32_t* n_sel, int32_t 
 /*
  * Sparse paged decode (finalize attention over selected blocks).  For each
  * (b, q row) the softmax of q . K^T * scale over the valid tokens of the blocks
- * idx[b, h, 0:n_sel[b,h]] (block_size tokens each), applied to V; split-K over
- * chunks of blocks with an online-softmax merge (CBT/page_attention.py:206-255,
- * CBT/legacy.py:765-794).  out: [batch, n_q_heads, D] contiguous, out_dtype
- * IA_F32 or IA_BF16.  Replaces the selected-page stream of
+ * idx[b, h, 0:n_sel[b,h]] (block_size tokens each), applied to V; split-K with an
+ * online-softmax merge (CBT/page_attention.py:206-255, CBT/legacy.py:765-794): one
+ * flat grid of about one workgroup per CU, each (b, h) row split into items in
+ * proportion to its 16-token subtiles.  out: [batch, n_q_heads, D] contiguous,
+ * out_dtype IA_F32 or IA_BF16.  batch * n_kv_heads must not exceed 8192
+ * (IA_ERR_UNSUPPORTED).  Replaces the selected-page stream of
  * _condition_block_finalize_attention_kernel for the top-k rule.
  */
 IA_API size_t ia_paged_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
@@ -296,11 +298,13 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
                                 size_t workspace_bytes, void* stream);
 
 /*
- * One top-k decode-attention layer call in two launches: block scores (as
- * ia_select_topk computes them, bit for bit) by a many-workgroup scorer, then the
- * paged finalize whose prologue stages each (sequence, kv head)'s score row in LDS
- * and applies ia_select_topk's rule (forced blocks, k or k_per_seq, ties to the
- * lower index) before streaming the chosen blocks; the split-K merge follows.
+ * One top-k decode-attention layer call: block scores (as ia_select_topk computes
+ * them, bit for bit) by a many-workgroup scorer whose first workgroup also writes
+ * the finalize's launch plan (items per (sequence, kv head) from the rule's block
+ * counts), then the paged finalize whose prologue stages each (sequence, kv head)'s
+ * score row in LDS and applies ia_select_topk's rule (forced blocks, k or k_per_seq,
+ * ties to the lower index) before streaming its share of the chosen blocks; the
+ * split-K merge follows.
  * Equal to ia_select_topk + ia_sparse_paged_decode.  idx/n_sel (optional,
  * together) receive the selection.  Requires nb_max <= 4096 and k_cap <= 512
  * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  Replaces the selection +
@@ -318,9 +322,10 @@ IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, co
                                  int32_t out_dtype, int32_t* idx, int32_t* n_sel, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
-/* Number of split-K items per (b, h) the two decode entry points use for the
- * given workload; size the decode workspace with it.  max_seq_len must bound
- * every seq_lens[b] passed to ia_paged_decode (tokens past it are not read). */
+/* Most split-K items per (b, h) the two decode entry points use for the given
+ * workload (the stride of the partials); size the decode workspace with it.
+ * Tokens of ia_paged_decode past max_seq_len (rounded up to a 128-token tile) are
+ * not read, whatever seq_lens holds. */
 IA_API int32_t ia_sparse_max_items(int32_t batch, int32_t n_kv_heads, int32_t k_cap);
 IA_API int32_t ia_dense_max_items(int32_t batch, int32_t n_kv_heads, int32_t max_seq_len);
 

@@ -157,7 +157,7 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   p.seq_lens = seq_lens;
   p.idx = idx;
   p.n_sel = n_sel;
-  p.k_cap = k_cap;
+  p.k_cap = sparse ? k_cap : (int32_t)units_max;  // dense: tiles of max_seq_len
   p.unit_tokens = unit_tokens;
   p.n_kv_heads = shape->n_kv_heads;
   p.sfx_len_stride = 0;

@@ -266,12 +266,14 @@ __device__ __forceinline__ float mfma_row_alpha(float alpha, int i, int lane) {
 // ------------------------------------------------------------ balanced launch plan
 // (plan.hpp).  Units of row r for the finalize's own plan: top-k, the row's selected
 // blocks; dense, its 128-token tiles.
+// Dense units are capped at k_cap = ceil(max_seq_len / tile): tokens past the host's
+// bound are never read, and no row needs more than max_items items.
 template <int SRC>
 __device__ __forceinline__ int plan_row_units(const DecodeParams& p, int r) {
   if constexpr (SRC == kSrcTopk) {
     return min(max(p.n_sel[r], 0), p.k_cap);
   } else {
-    return cdiv_pos(max(p.seq_lens[r / p.n_kv_heads], 0), p.unit_tokens);
+    return min(cdiv_pos(max(p.seq_lens[r / p.n_kv_heads], 0), p.unit_tokens), p.k_cap);
   }
 }
 

@@ -99,3 +99,22 @@ def test_plan_one_long_row(device):
     case = make_case(seed=31337, batch=len(lens), hq=hq, hkv=hkv, d=d, seq_lens=lens, page_size=16)
     kvec = [400, 1, 2]
     _run(case, device, hq, hkv, block, kvec, sample=range(len(lens)), dense_sample=range(len(lens)))
+
+
+def test_dense_reads_nothing_past_max_seq_len(device):
+    """A sequence longer than the launch's max_seq_len: the dense plan caps its tiles
+    at ceil(max_seq_len / 128), so the call reads (and attends) the first 1024 tokens
+    only and every row keeps its items within the partial stride."""
+    announce("balanced plan: dense past max_seq_len")
+    lens = [700, 5000]
+    hq, hkv, d = 8, 2, 128
+    case = make_case(seed=6060, batch=2, hq=hq, hkv=hkv, d=d, seq_lens=lens, page_size=16)
+    dev = to_dev(case, device)
+    out = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                          max_seq_len=1000, workspace={})
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    ref0 = A.dense_decode(case["q"][0], case["k"][0], case["v"][0])
+    ref1 = A.dense_decode(case["q"][1], case["k"][1][:, :1024], case["v"][1][:, :1024])
+    assert np.abs(got[0] - ref0).max() <= 2e-2
+    assert np.abs(got[1] - ref1).max() <= 2e-2

@@ -86,7 +86,7 @@ __device__ __forceinline__ u32 wave_u32_max(u32 v) {
 // Exclusive prefix sum of one int per thread over the workgroup (thread order);
 // *total receives the sum.  Every thread calls it; two barriers.
 template <int NT>
-__device__ __forceinline__ int block_exclusive_scan(int v, int* wsum, int* total) {
+__device__ __forceinline__ int block_exclusive_scan(int v, int* wsum, int* total, bool reuse = true) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int inc = wave_inclusive_scan(v);
@@ -99,7 +99,8 @@ __device__ __forceinline__ int block_exclusive_scan(int v, int* wsum, int* total
     tot += s;
     before += (w < wave) ? s : 0;
   }
-  __syncthreads();
+  // reuse false (a uniform value): the caller synchronises before wsum is written again
+  if (reuse) __syncthreads();
   *total = tot;
   return before + inc - v;
 }
@@ -262,23 +263,43 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
           }
         }
         __syncthreads();
-        // member i's rank among the bucket's members; rank need - 1 is the threshold
-        for (int i = threadIdx.x; i < in_bin; i += NT) {
-          const u32 ki = L.tie_key[i];
-          const int ji = L.tie_idx[i];
+        // member i's rank among the bucket's members (key descending, then index
+        // ascending: a strict order, so ranks are distinct); rank need - 1 is the threshold
+        if (in_bin <= 64) {
+          // every wave ranks the members from registers (lane i holds member i), so no
+          // LDS round trip per member and no barrier before the threshold is known
+          const int lane = threadIdx.x & 63;
+          const bool mem = lane < in_bin;
+          const u32 ki = mem ? L.tie_key[lane] : 0u;
+          const int ji = mem ? L.tie_idx[lane] : 0;
           int rank = 0;
           for (int e = 0; e < in_bin; ++e) {
-            const u32 ke = L.tie_key[e];
-            rank += (ke > ki || (ke == ki && L.tie_idx[e] < ji)) ? 1 : 0;
+            const u32 ke = (u32)__builtin_amdgcn_readlane((int)ki, e);
+            const int je = __builtin_amdgcn_readlane(ji, e);
+            rank += (ke > ki || (ke == ki && je < ji)) ? 1 : 0;
           }
-          if (rank == need - 1) {
-            L.thr_key = ki;
-            L.thr_idx = ji;
+          const unsigned long long hit = __ballot(mem && rank == need - 1);
+          const int src = __ffsll((long long)hit) - 1;
+          kT = (u32)__builtin_amdgcn_readlane((int)ki, src);
+          iT = __builtin_amdgcn_readlane(ji, src);
+        } else {
+          for (int i = threadIdx.x; i < in_bin; i += NT) {
+            const u32 ki = L.tie_key[i];
+            const int ji = L.tie_idx[i];
+            int rank = 0;
+            for (int e = 0; e < in_bin; ++e) {
+              const u32 ke = L.tie_key[e];
+              rank += (ke > ki || (ke == ki && L.tie_idx[e] < ji)) ? 1 : 0;
+            }
+            if (rank == need - 1) {
+              L.thr_key = ki;
+              L.thr_idx = ji;
+            }
           }
+          __syncthreads();
+          kT = L.thr_key;
+          iT = L.thr_idx;
         }
-        __syncthreads();
-        kT = L.thr_key;
-        iT = L.thr_idx;
       } else {
         fast = false;
       }
@@ -360,7 +381,8 @@ __device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule&
       }
     }
     int total;
-    int pos = base_sel + block_exclusive_scan<NT>(__popc(bits), L.wsum, &total);
+    // the last chunk's scan needs no second barrier: the one below comes first
+    int pos = base_sel + block_exclusive_scan<NT>(__popc(bits), L.wsum, &total, c0 + NT * seg < nb);
     while (bits) {
       const int e = __ffs((int)bits) - 1;
       bits &= bits - 1u;

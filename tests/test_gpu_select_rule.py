@@ -11,6 +11,11 @@ repeated k_bar rows so that exact ties are frequent:
 * ``zero``: every score equal (the whole row is one tie);
 * ``crowd``: random rows plus 400 copies of the best one (a crowded threshold
   bucket: the radix fallback and its tie scan);
+* ``crowd100``: 100 copies of the best row (a threshold bucket of 65..128 members,
+  ranked through LDS);
+* ``crowd40``: 40 copies of the best row at three nearby scales (a threshold bucket
+  of at most 64 members, ranked from registers in every wave; ties and distinct
+  keys);
 * ``inf``: positive queries and rows of +-3e38 (scores of +-inf, the non-finite
   fallback);
 * ``far``: random rows plus a few scaled by 1e6 (a huge range, most candidates in
@@ -34,7 +39,7 @@ from tests._util import announce
 pytestmark = pytest.mark.gpu
 
 HQ, HKV, D, BLOCK, PAGE = 8, 2, 64, 16, 16
-PATTERNS = ["dup5", "zero", "crowd", "inf", "far", "random"]
+PATTERNS = ["dup5", "zero", "crowd", "inf", "far", "random", "crowd100", "crowd40"]
 RULES = [(37, 0, 0, False), (37, 2, 3, False), (40, 1, 2, True)]
 
 
@@ -46,11 +51,14 @@ def _rows(pattern, nb, rng):
         kb = base[:, rng.integers(0, 5, nb)]
     elif pattern == "zero":
         kb[:] = 0.0
-    elif pattern == "crowd":
+    elif pattern in ("crowd", "crowd100", "crowd40"):
+        m = {"crowd": 400, "crowd100": 100, "crowd40": 40}[pattern]
         qm = q.reshape(HKV, HQ // HKV, D).sum(1)
         for h in range(HKV):
             best = kb[h, np.argmax(kb[h] @ qm[h])].copy()
-            kb[h, rng.choice(nb, 400, replace=False)] = best
+            pick = rng.choice(nb, m, replace=False)
+            scale = rng.choice([1.0, 1.0 - 1.0 / 128, 1.0 - 1.0 / 64], m) if pattern == "crowd40" else np.ones(m)
+            kb[h, pick] = best[None] * scale[:, None].astype(np.float32)
     elif pattern == "inf":
         q = np.abs(q) + 0.1
         pick = rng.choice(nb, 60, replace=False)

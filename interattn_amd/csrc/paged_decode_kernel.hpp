@@ -40,6 +40,7 @@
 #pragma once
 
 #include <algorithm>
+#include <atomic>
 
 #include "plan.hpp"
 #include "topk_select.hpp"
@@ -1328,21 +1329,27 @@ int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
   return check_launch("split-k merge");
 }
 
-// Resident workgroups of one instance on the current device (cached).
+// Resident workgroups of one instance on the current device, cached per device
+// (relaxed atomics: concurrent first calls compute the same value).  0 on a query
+// failure (the callers then assume 1024).
+constexpr int kMaxCachedDevices = 64;
 template <int D, int G, typename KV, int SRC>
 int resident_wgs() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
+  static std::atomic<int> cached[kMaxCachedDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  int n = dev < kMaxCachedDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
             &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC>), kFinThreads,
             0) != hipSuccess)
       return 0;
-    cached = std::max(1, cus * per_cu);
+    n = std::max(1, cus * per_cu);
+    if (dev < kMaxCachedDevices) cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached;
+  return n;
 }
 
 // Host helpers shared by the decode entry points (paged_decode.hip).

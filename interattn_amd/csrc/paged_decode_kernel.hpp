@@ -501,8 +501,19 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   const int page_size = kv.page_size;
   const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
 
-  // ---- prologue: token ranges of this item's units, then one page id per subtile
-  for (int t = threadIdx.x; t < nu; t += kFinThreads) {
+  // ---- prologue: token ranges of this item's units (the fused source computes them
+  // from its LDS selection where they are used), then one page id per subtile
+  auto fused_range = [&](int ul, int& lo, int& hi) {
+    const int u = u_begin + ul;
+    const int j = u >= n_units ? -1 : fsel[u];
+    lo = 0;
+    hi = 0;
+    if (j >= 0 && (int64_t)j * p.unit_tokens < seq_len) {
+      lo = j * p.unit_tokens;
+      hi = min(lo + p.unit_tokens, seq_len);
+    }
+  };
+  for (int t = threadIdx.x; SRC != kSrcTopkFused && t < nu; t += kFinThreads) {
     const int u = u_begin + t;
     int lo = 0, hi = 0, sfx = 0;
     if constexpr (SRC == kSrcTopk || SRC == kSrcTopkFused) {
@@ -540,7 +551,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     unit_lo[t] = lo;
     unit_hi[t] = sfx ? -hi - 1 : hi;  // suffix units carry a negative end
   }
-  __syncthreads();
+  if constexpr (SRC != kSrcTopkFused) __syncthreads();  // fused: fsel is synchronised
   // valid subtiles of the item's raw slots in ascending order, compacted (ballots +
   // per-wave counts)
   int n_sub = 0;  // uniform
@@ -550,8 +561,13 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     int pg = kNoPage, info = 0;
     if (t < nu * nsub_u && raw0 + t >= slot_lo && raw0 + t < slot_hi) {
       const int u = t / nsub_u;
-      const int lo = unit_lo[u];
-      const int hi_raw = unit_hi[u];
+      int lo, hi_raw;
+      if constexpr (SRC == kSrcTopkFused) {
+        fused_range(u, lo, hi_raw);
+      } else {
+        lo = unit_lo[u];
+        hi_raw = unit_hi[u];
+      }
       const bool sfx = hi_raw < 0;
       const int hi = sfx ? -hi_raw - 1 : hi_raw;
       const int tok = lo + 16 * (t - u * nsub_u);

@@ -601,11 +601,9 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
 #pragma unroll
     for (int w = 0; w < kFinWaves; ++w) n_sub += wcnt_p[w];
-    __syncthreads();
+    __syncthreads();  // also publishes the last pass's sub_pg / sub_info to the stream
   }
   n_sub = __builtin_amdgcn_readfirstlane(n_sub);
-
-  __syncthreads();
 
   const char* kbase = reinterpret_cast<const char*>(kv.k) + (int64_t)h * kv.k_head_stride * KV::kBytes;
   const char* vbase = reinterpret_cast<const char*>(kv.v) + (int64_t)h * kv.v_head_stride * KV::kBytes;

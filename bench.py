@@ -33,11 +33,16 @@ import interattn_amd as ia  # noqa: E402
 HBM_PEAK_GBPS = 8000.0
 
 WORKLOADS = {
-    # name: batch, hq, hkv, d, seq_len (or "c3"), page, block, k, forced_first, forced_last, kv dtype
-    "c4": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="bf16"),
-    "c5": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="fp8"),
-    "c2": dict(batch=1, hq=32, hkv=8, d=128, seq=32768, page=16, block=64, k=64, ff=1, fl=2, kv="bf16"),
-    "c3": dict(batch=16, hq=32, hkv=8, d=128, seq="c3", page=16, block=64, k=None, ff=0, fl=0, kv="bf16"),
+    # name: batch, hq, hkv, d, seq_len (or "c3"), page, block, k, forced_first, forced_last, kv dtype,
+    # per-(kv head, channel) key outlier scale, seed
+    "c4": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="bf16",
+               seed=1237),
+    "c5": dict(batch=16, hq=32, hkv=8, d=128, seq=131072, page=16, block=128, k=64, ff=0, fl=0, kv="fp8",
+               seed=1237),
+    "c2": dict(batch=1, hq=32, hkv=8, d=128, seq=32768, page=16, block=64, k=64, ff=1, fl=2, kv="bf16",
+               k_outlier=True, seed=1235),
+    "c3": dict(batch=16, hq=32, hkv=8, d=128, seq="c3", page=16, block=64, k=None, ff=0, fl=0, kv="bf16",
+               seed=1237),
     # the reference's own routing rule (eps threshold) at its published configuration: batch 1,
     # block 64, mixed summaries with bf16 k_bar, one suffix token, eps set so that the
     # fraction of selected blocks matches the reference's run at that length
@@ -60,7 +65,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of hipGraph replay")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-seqs", type=int, default=2)
+    ap.add_argument("--extra", default="c5,c3,c2",
+                    help="other BASELINE configs timed in the same run and reported under 'extra' "
+                         "(comma list; empty for none)")
     return ap.parse_args()
 
 
@@ -87,6 +94,10 @@ def make_layer(w, dev, gen, lens, table, n_pages):
         pool_k = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
         pool_v = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
         scales = None
+    if w.get("k_outlier"):
+        # C2: keys scaled per (kv head, channel) by exp(N(0,1)) ("RoPE'd keys")
+        outlier = torch.randn((hkv, d), device=dev, generator=gen).exp()
+        pool_k.mul_(outlier[None, :, None, :].to(pool_k.dtype))
     q = torch.randn((w["batch"], w["hq"], d), device=dev, dtype=torch.bfloat16, generator=gen)
     seq_lens = torch.tensor(lens, device=dev, dtype=torch.int32)
     nb_max = max(math.ceil(L / w["block"]) for L in lens)
@@ -154,71 +165,90 @@ def time_events(fn, n, stream):
     return start.elapsed_time(end) / n
 
 
-def cpu_baseline(w, L0, table, lens, idx_host, nsel_host, n_seqs):
-    """The oracle (numpy restatement of the reference's CPU path) on a bounded sample:
-    ``n_seqs`` sequences of layer 0, all KV heads: top-k scores from the cached k_bar
-    summaries, selection, then attention over the gathered selected tokens.  Returns
-    microseconds per full layer call (scaled by batch / n_seqs)."""
-    import numpy as np
-
-    from oracle import attention as A
-    from oracle import select as S
-
-    d, hq, hkv, block, page = w["d"], w["hq"], w["hkv"], w["block"], w["page"]
-    g = hq // hkv
-    pool_k = L0["pool_k"]
-    pool_v = L0["pool_v"]
-    inputs = []
-    for b in range(n_seqs):
-        nb = math.ceil(lens[b] / block)
-        kb = L0["k_bar"][b, :, :nb].float().cpu().numpy()
-        q = L0["q"][b].float().cpu().numpy()
-        kv_blocks = {}
-        for h in range(hkv):
-            for j in idx_host[b][h][:nsel_host[b][h]]:
-                pages = table[b, j * block // page:(j * block + block) // page].long()
-                kv_blocks[(h, int(j))] = (pool_k[pages, h].float().reshape(-1, d).cpu().numpy(),
-                                          pool_v[pages, h].float().reshape(-1, d).cpu().numpy())
-        inputs.append((q, kb, nb, kv_blocks))
-    counts_full = None
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        for q, kb, nb, kv_blocks in inputs:
-            counts = np.full(nb, block)
-            sc = S.topk_block_scores(q, kb, counts, g)
-            for h in range(hkv):
-                sel = S.select_topk(sc[h], nb, w["k"] or max(16, nb // 16), w["ff"], w["fl"], False)
-                ks = np.concatenate([kv_blocks[(h, int(j))][0] for j in sel if (h, int(j)) in kv_blocks] or
-                                    [np.zeros((0, d))])
-                vs = np.concatenate([kv_blocks[(h, int(j))][1] for j in sel if (h, int(j)) in kv_blocks] or
-                                    [np.zeros((0, d))])
-                A.dense_decode(q[h * g:(h + 1) * g], ks[None], vs[None])
-        reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 1000:  # about 10 s of CPU work
-            break
-    dt = (time.perf_counter() - t0) / reps
-    del counts_full
-    return dt / n_seqs * len(lens) * 1e6, reps
+def time_repeats(run, n_runs, steps_per_run, stream, max_repeats=10):
+    """Time ``n_runs`` back-to-back calls of ``run`` (each ``steps_per_run`` steps) as
+    ``min(n_runs, max_repeats)`` repeats of equal length, one HIP event pair per repeat
+    on ``stream``, the whole region bracketed by device synchronisations (an event
+    pair costs about 3 us of stream time, so a repeat groups several runs when there
+    are many).  Returns (per-step microseconds of each repeat, steps timed)."""
+    repeats = min(n_runs, max_repeats)
+    per_rep = n_runs // repeats
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(repeats)]
+    torch.cuda.synchronize()
+    for s_, e_ in evs:
+        s_.record(stream)
+        for _ in range(per_rep):
+            run()
+        e_.record(stream)
+    torch.cuda.synchronize()
+    per = [s_.elapsed_time(e_) * 1e3 / (per_rep * steps_per_run) for s_, e_ in evs]
+    return per, repeats * per_rep * steps_per_run
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
-        sys.exit(2)
-    w = dict(WORKLOADS[args.workload])
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    if w.get("mode") == "cond":
-        return main_condition(args, w, dev)
+def spread(per_step_us):
+    v = sorted(per_step_us)
+    n = len(v)
+    return {"repeats": n, "median_us": round(v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2]), 3),
+            "min_us": round(v[0], 3), "max_us": round(v[-1], 3), "mean_us": round(sum(v) / n, 3)}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(w, L0, table, lens, k_cap, gpu_out, runs=5):
+    """The reference's CPU PyTorch path on the host cores: for every sequence of one
+    layer call, group-mean block scores from the cached k_bar, top-k selection, the
+    gather of the chosen blocks' K/V out of the paged pool through the block table,
+    and fp32 attention (``oracle.torch_path``, pinned against the numpy oracle).  Each
+    sequence is timed on its own and the batch summed; the value is the median of
+    ``runs`` timed passes after one warm-up pass.  Also returns the largest
+    difference from the GPU output (a cross-check of the two paths)."""
+    from oracle import torch_path as T
+
+    cpu = torch.device("cpu")
+    pk = L0["pool_k"].to(cpu)
+    pv = L0["pool_v"].to(cpu)
+    scales = None if L0["scales"] is None else tuple(x.to(cpu) for x in L0["scales"])
+    kb = L0["k_bar"].to(cpu)
+    q = L0["q"].to(cpu)
+    tab = table.to(cpu)
+    kk = [w["k"] if w["k"] else max(16, math.ceil(Ln / w["block"]) // 16) for Ln in lens]
+
+    def one_pass():
+        per_seq = []
+        outs = []
+        for b, Ln in enumerate(lens):
+            t0 = time.perf_counter()
+            o, _ = T.topk_layer_call(q[b], pk, pv, tab[b], Ln, kb[b], block=w["block"], page=w["page"], k=kk[b],
+                                     forced_first=w["ff"], forced_last=w["fl"], scales=scales)
+            per_seq.append(time.perf_counter() - t0)
+            outs.append(o)
+        return sum(per_seq), outs
+
+    _, outs = one_pass()
+    times = sorted(one_pass()[0] for _ in range(runs))
+    err = max(float((o - gpu_out[b].float().cpu()).abs().max()) for b, o in enumerate(outs))
+    return times[len(times) // 2] * 1e6, times, err
+
+
+def run_topk(name, args, dev, with_dense, with_cpu):
+    """Time one top-k workload; returns the result dict (the JSON line's fields)."""
+    w = dict(WORKLOADS[name])
     lens = c3_lengths() if w["seq"] == "c3" else [w["seq"]] * w["batch"]
     w["batch"] = len(lens)
     pages_per = [math.ceil(L / w["page"]) for L in lens]
     n_pages = sum(pages_per)
     max_pages = max(pages_per)
     gen = torch.Generator(device=dev)
-    gen.manual_seed(1237)
+    gen.manual_seed(w["seed"])
     perm = torch.randperm(n_pages, device=dev, generator=gen).to(torch.int32)
     table = torch.full((len(lens), max_pages), -1, device=dev, dtype=torch.int32)
     off = 0
@@ -234,11 +264,11 @@ def main():
     t_setup = time.perf_counter()
     layers = [make_layer(w, dev, gen, lens, table, n_pages) for _ in range(args.layers)]
     torch.cuda.synchronize()
-    setup_s = time.perf_counter() - t_setup
-    print(f"[bench] workload={args.workload} layers={args.layers} setup {setup_s:.1f}s", file=sys.stderr, flush=True)
+    print(f"[bench] workload={name} layers={args.layers} setup {time.perf_counter() - t_setup:.1f}s",
+          file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream()
-    # selection results of layer 0 (for byte accounting and the CPU baseline)
+    # selection results of layer 0 (for the byte accounting)
     _, idx0, nsel0 = layer_call(layers[0], w, table, kvec, k_cap, selection=True)
     torch.cuda.synchronize()
     idx_h = idx0.cpu().numpy()
@@ -246,9 +276,10 @@ def main():
     sel_lists = [[idx_h[b, h, :nsel_h[b, h]] for h in range(w["hkv"])] for b in range(len(lens))]
     qo_b, summ_b, kv_b = algorithmic_bytes(w, lens, sel_lists)
     total_bytes = qo_b + summ_b + kv_b
+    gpu_out0 = layers[0]["out"].clone()
 
     # warmup (also builds every workspace before capture)
-    for i in range(args.warmup):
+    for _ in range(args.warmup):
         for L in layers:
             layer_call(L, w, table, kvec, k_cap)
     torch.cuda.synchronize()
@@ -278,28 +309,23 @@ def main():
             use_graph = False
 
     nl = len(layers)
-    replays = max(1, args.steps // nl)
-    steps = replays * nl
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    if use_graph:
-        for _ in range(replays):
+    replays = max(5, args.steps // nl)
+
+    def run_replay():
+        if use_graph:
             graph.replay()
-    else:
-        for _ in range(replays):
+        else:
             for L in layers:
                 layer_call(L, w, table, kvec, k_cap)
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = start.elapsed_time(end)
-    us_per_layer = ms_total * 1e3 / steps
 
-    # per-call averages (eager back-to-back launches on this stream): the fused layer
-    # call, and the two-step path's selection and finalize (+ merge) on the same data
+    t0 = time.perf_counter()
+    per_step, steps = time_repeats(run_replay, replays, nl, stream)
+    wall = time.perf_counter() - t0
+    tim = spread(per_step)
+    us_per_layer = tim["median_us"]
+
+    # eager back-to-back calls on the launch stream (no graph), and the two-step path
+    # (selection, then finalize + merge) on the same data
     nrep = max(8, args.steps // (2 * nl))
 
     def run_call():
@@ -325,12 +351,12 @@ def main():
     call_us = time_events(run_call, nrep, stream) * 1e3 / nl
     sel_us = time_events(run_select, nrep, stream) * 1e3 / nl
     fin_us = time_events(run_finalize, nrep, stream) * 1e3 / nl
-    call_gbps = total_bytes / (call_us * 1e-6) / 1e9
     fin_bytes = qo_b + kv_b
-    fin_gbps = fin_bytes / (fin_us * 1e-6) / 1e9
 
     dense_us = None
-    if not args.no_dense:
+    s_kv = 1 if w["kv"] == "fp8" else 2
+    dense_bytes = qo_b + sum(w["hkv"] * L * w["d"] * 2 * s_kv for L in lens)
+    if with_dense:
         L = layers[0]
         ia.paged_decode(L["q"], L["pool_k"], L["pool_v"], table, L["seq_lens"], max_seq_len=max(lens),
                         scales=L["scales"], out=L["out"], workspace=L["ws"])
@@ -343,66 +369,113 @@ def main():
 
         dense_us = time_events(run_dense, 3, stream) * 1e3 / nl
 
-    copy_gbps = copy_ceiling_gbps(dev)
-    s_kv = 1 if w["kv"] == "fp8" else 2
-    dense_bytes = qo_b + sum(w["hkv"] * L * w["d"] * 2 * s_kv for L in lens)
-
     cpu = None
-    if not args.no_cpu_baseline:
-        n_s = min(args.cpu_sample_seqs, len(lens))
-        cpu_us, reps = cpu_baseline(w, layers[0], table, lens, idx_h, nsel_h, n_s)
-        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
-               "sample": f"{n_s} of {len(lens)} sequences of one layer call, all {w['hkv']} KV heads "
-                         f"(numpy oracle: scores from cached k_bar, top-k, attention over gathered selected "
-                         f"tokens), {reps} reps, scaled by {len(lens)}/{n_s}",
-               "cpu": platform.processor() or platform.machine()}
+    if with_cpu:
+        cpu_us, cpu_runs, cpu_err = cpu_baseline(w, layers[0], table, lens, k_cap, gpu_out0)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"the whole layer call: all {len(lens)} sequences x {w['hkv']} KV heads, each sequence "
+                         f"timed on its own (scores from cached k_bar, top-k, gather of the chosen blocks through "
+                         f"the block table, fp32 attention; torch CPU, oracle/torch_path.py) and summed; median "
+                         f"of {len(cpu_runs)} passes after one warm-up pass "
+                         f"(min {min(cpu_runs) * 1e6:.0f}, max {max(cpu_runs) * 1e6:.0f} us)",
+               "cpu": cpu_model(), "os_cpu_count": os.cpu_count(),
+               "max_abs_diff_vs_gpu": round(cpu_err, 6)}
 
-    # HBM bytes per finalize launch measured by rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated)
-    traffic = traffic_src = None
+    del layers, graph
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    gbps = total_bytes / (us_per_layer * 1e-6) / 1e9
+    return dict(w=w, lens=lens, steps=steps, us=us_per_layer, timing=tim, wall=wall, use_graph=use_graph, nl=nl,
+                total_bytes=total_bytes, qo_b=qo_b, summ_b=summ_b, kv_b=kv_b, gbps=gbps, call_us=call_us,
+                sel_us=sel_us, fin_us=fin_us, fin_bytes=fin_bytes, dense_us=dense_us, dense_bytes=dense_bytes,
+                cpu=cpu)
+
+
+def traffic_of(name):
+    """HBM bytes per layer call measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (copy-calibrated), from profiles/hbm_traffic.json."""
     tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if os.path.exists(tpath):
-        rec = json.load(open(tpath)).get(args.workload)
+        rec = json.load(open(tpath)).get(name)
         if rec:
-            traffic = int(round(rec["hbm_read_bytes"] + rec["hbm_write_bytes"]))
-            traffic_src = rec["source"]
+            return int(round(rec["hbm_read_bytes"] + rec["hbm_write_bytes"])), rec["source"]
+    return None, None
 
+
+def config_of(name, r):
+    w, lens = r["w"], r["lens"]
+    return {"workload": f"BASELINE config {name[1:]}", "batch": len(lens),
+            "seq_len": lens[0] if len(set(lens)) == 1 else f"ragged {min(lens)}..{max(lens)}",
+            "q_heads": w["hq"], "kv_heads": w["hkv"], "head_dim": w["d"], "kv_block": w["block"],
+            "page": w["page"], "top_k": w["k"] if w["k"] else "max(16, nb/16)",
+            "forced_first": w["ff"], "forced_last": w["fl"], "kv_dtype": w["kv"],
+            "k_outlier": bool(w.get("k_outlier")), "layers_rotated": r["nl"],
+            "launch": "hipgraph" if r["use_graph"] else "eager"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        sys.exit(2)
+    w = dict(WORKLOADS[args.workload])
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if w.get("mode") == "cond":
+        return main_condition(args, w, dev)
+    name = args.workload
+    r = run_topk(name, args, dev, with_dense=not args.no_dense, with_cpu=not args.no_cpu_baseline)
+    copy_gbps = copy_ceiling_gbps(dev)
+    traffic, traffic_src = traffic_of(name)
+    extra = {}
+    for other in [x for x in args.extra.split(",") if x and x != name]:
+        e = run_topk(other, args, dev, with_dense=False, with_cpu=False)
+        t_o, _ = traffic_of(other)
+        extra[other] = {"config": config_of(other, e), "value": e["us"], "unit": "us/layer", "timing": e["timing"],
+                        "algorithmic_bytes": e["total_bytes"], "achieved_GBps": round(e["gbps"], 1),
+                        "frac": round(e["gbps"] / HBM_PEAK_GBPS, 4), "traffic": t_o,
+                        "eager_call_us": round(e["call_us"], 3)}
+    us = r["us"]
+    w = r["w"]
     dtype = "fp8e4m3-kv/bf16-q" if w["kv"] == "fp8" else "bf16"
     line = {
-        "metric": "\u00b5s per decode-attn layer + achieved HBM GB/s (% peak), 32K\u2013128K ctx",
-        "value": round(us_per_layer, 3),
+        "metric": "µs per decode-attn layer + achieved HBM GB/s (% peak), 32K–128K ctx",
+        "value": round(us, 3),
         "unit": "us/layer",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": r["steps"],
         "warmup": args.warmup,
-        "ms_per_step": round(us_per_layer / 1e3, 6),
+        "ms_per_step": round(us / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dtype,
-        "data": "synthetic N(0,1) q/K/V, random page permutation, seed 1237",
-        "config": {"workload": f"BASELINE config {args.workload[1:]}", "batch": len(lens),
-                   "seq_len": lens[0] if len(set(lens)) == 1 else f"ragged {min(lens)}..{max(lens)}",
-                   "q_heads": w["hq"], "kv_heads": w["hkv"], "head_dim": w["d"], "kv_block": w["block"],
-                   "page": w["page"], "top_k": w["k"] if w["k"] else "max(16, nb/16)",
-                   "forced_first": w["ff"], "forced_last": w["fl"], "layers_rotated": nl,
-                   "launch": "hipgraph" if use_graph else "eager"},
-        "achieved_GBps": round(total_bytes / (us_per_layer * 1e-6) / 1e9, 1),
-        "pct_hbm_peak": round(100 * total_bytes / (us_per_layer * 1e-6) / 1e9 / HBM_PEAK_GBPS, 2),
-        "algorithmic_bytes": {"total": total_bytes, "q_out": qo_b, "k_bar": summ_b, "selected_kv": kv_b},
-        "kernels_us": {"ia_sparse_topk_decode": round(call_us, 3), "two_step_select_topk": round(sel_us, 3),
-                       "two_step_finalize_merge": round(fin_us, 3)},
+        "data": f"synthetic N(0,1) q/K/V, random page permutation, seed {w['seed']}",
+        "config": config_of(name, r),
+        "timing": {**r["timing"], "steps_timed": r["steps"],
+                   "note": "value = median per-step time over the repeats; a repeat = one or more hipGraph replays "
+                           "of the rotated layers"},
+        "achieved_GBps": round(r["gbps"], 1),
+        "pct_hbm_peak": round(100 * r["gbps"] / HBM_PEAK_GBPS, 2),
+        "algorithmic_bytes": {"total": r["total_bytes"], "q_out": r["qo_b"], "k_bar": r["summ_b"],
+                              "selected_kv": r["kv_b"]},
+        "kernels_us": {"ia_sparse_topk_decode_eager": round(r["call_us"], 3),
+                       "two_step_select_topk": round(r["sel_us"], 3),
+                       "two_step_finalize_merge": round(r["fin_us"], 3)},
         "roofline": {"bound": "hbm",
-                     "kernel": "ia_sparse_topk_decode (topk_scores + paged_finalize + splitk_merge launches)",
-                     "achieved": round(call_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(call_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "traffic_source": traffic_src},
-        "two_step_finalize_GBps": round(fin_gbps, 1),
+                     "kernel": "ia_sparse_topk_decode (one layer call: every launch it makes)",
+                     "achieved": round(r["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(r["gbps"] / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
+                     "timed": "the same median graph-replay time as value"},
+        "two_step_finalize_GBps": round(r["fin_bytes"] / (r["fin_us"] * 1e-6) / 1e9, 1),
         "copy_ceiling_GBps": round(copy_gbps, 1),
-        "dense_us": None if dense_us is None else round(dense_us, 2),
-        "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
-        "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us_per_layer, 2),
-        "cpu_baseline": cpu,
-        "wall_s": round(wall, 3),
+        "dense_us": None if r["dense_us"] is None else round(r["dense_us"], 2),
+        "dense_GBps": None if r["dense_us"] is None else round(r["dense_bytes"] / (r["dense_us"] * 1e-6) / 1e9, 1),
+        "sparse_vs_dense_speedup": None if r["dense_us"] is None else round(r["dense_us"] / us, 2),
+        "cpu_baseline": r["cpu"],
+        "extra": extra,
+        "wall_s": round(r["wall"], 3),
     }
     print(json.dumps(line), flush=True)
 
@@ -521,24 +594,21 @@ def main_condition(args, w, dev):
             print("[bench] graph replay mismatch; timing eager launches", file=sys.stderr, flush=True)
             use_graph = False
     nl = len(layers)
-    replays = max(1, args.steps // nl)
-    steps = replays * nl
+    replays = max(5, args.steps // nl)
     stream = torch.cuda.current_stream()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(replays):
+
+    def run_replay():
         if use_graph:
             graph.replay()
         else:
             for L in layers:
                 call(L)
-    end.record(stream)
-    torch.cuda.synchronize()
+
+    t0 = time.perf_counter()
+    per_step, steps = time_repeats(run_replay, replays, nl, stream)
     wall = time.perf_counter() - t0
-    us = start.elapsed_time(end) * 1e3 / steps
+    tim = spread(per_step)
+    us = tim["median_us"]
 
     dense_us = None
     if not args.no_dense:
@@ -556,8 +626,8 @@ def main_condition(args, w, dev):
         cpu_us, reps = condition_cpu_baseline(w, layers[0], eps)
         cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
                "sample": f"one full layer call (batch 1), {reps} reps: numpy oracle of the eager selection and "
-                         f"the dense hybrid attention",
-               "cpu": platform.processor() or platform.machine()}
+                         f"the dense hybrid attention (single-threaded numpy)",
+               "cpu": cpu_model()}
     gbps = total / (us * 1e-6) / 1e9
     line = {
         "metric": "\u00b5s per decode-attn layer + achieved HBM GB/s (% peak), 32K\u2013128K ctx",
@@ -578,6 +648,7 @@ def main_condition(args, w, dev):
                    "kv_heads": hkv, "head_dim": d, "kv_block": block, "suffix": s, "eps": eps,
                    "selected_frac": round(frac, 5), "summaries": "mixed, bf16 k_bar", "layers_rotated": nl,
                    "launch": "hipgraph" if use_graph else "eager"},
+        "timing": {**tim, "steps_timed": steps},
         "achieved_GBps": round(gbps, 1),
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes": {"total": total, "q_out": qo_b, "summaries": summ_b, "representatives": rep_b,

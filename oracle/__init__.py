@@ -22,6 +22,11 @@ paged.paged_gather / scatter           brute-force loop + permutation invariance
 summaries.build_block_summaries        per-block brute-force loops, invariants,
                                        golden fixtures from the reference
 select.topk_block_scores/select_topk   brute-force sort, forced-block rules
+select.quest_block_scores              upper bound of every token's score,
+                                       one-token blocks, all-positive /
+                                       all-negative query closed forms
+torch_path.topk_layer_call             the numpy oracle above (selection
+                                       exact, outputs to float32 rounding)
 select.select_condition_eager          golden fixtures from the reference,
                                        eps=0 / eps=1e9 closed forms
 select.selection_stats_chunked         chunked LSE == global LSE, golden s/delta
@@ -35,3 +40,5 @@ attention.splitk_merge                 n_chunks=1 identity, chunking invariance
 """
 
 from . import numerics, paged, summaries, select, attention  # noqa: F401
+
+# torch_path (the timed CPU baseline) is imported on demand: it needs torch

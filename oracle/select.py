@@ -34,6 +34,25 @@ def topk_block_scores(q, k_bar, counts, group):
     return s
 
 
+def quest_block_scores(q, k_max, k_min, group):
+    """``q [Hq, D]``, ``k_max, k_min [Hkv, nb, D]`` -> ``[Hkv, nb]`` float64.
+
+    The Quest page score (CBG/methods/quest.py:97-101): per query head,
+    ``sum_d max(q_d * k_max_d, q_d * k_min_d)`` (an upper bound of ``q . k_t`` over the
+    block's tokens, no ``1/sqrt(D)``), then the mean over the GQA group.  Blocks with
+    no valid token (``k_max = -inf``) score -inf.
+    """
+    hq, d = q.shape
+    hkv = k_max.shape[0]
+    qg = q.astype(np.float64).reshape(hkv, group, 1, d)
+    kx = k_max.astype(np.float64)[:, None]
+    kn = k_min.astype(np.float64)[:, None]
+    with np.errstate(invalid="ignore"):
+        s = np.maximum(qg * kx, qg * kn).sum(-1).mean(axis=1)
+    s[~np.isfinite(k_max.astype(np.float64)).all(-1)] = -np.inf
+    return s
+
+
 def forced_blocks(nb_valid, forced_first, forced_last):
     f = set(range(min(int(forced_first), nb_valid)))
     f |= set(range(max(nb_valid - int(forced_last), 0), nb_valid))

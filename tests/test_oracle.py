@@ -142,6 +142,38 @@ def test_topk_scores_brute_force():
             assert abs(got[h, j] - s / 4.0) < 1e-9
 
 
+def test_quest_scores_bound_and_closed_forms():
+    """The Quest page score is pinned by what it must satisfy, not by its formula:
+    (1) it bounds the group-mean q . k_t of every token of the block from above;
+    (2) a one-token block (k_max = k_min = k) scores exactly mean_g q_g . k;
+    (3) a group whose queries are all >= 0 scores mean_g q_g . k_max, all <= 0
+    mean_g q_g . k_min; (4) empty blocks score -inf."""
+    rng = np.random.default_rng(21)
+    hq, hkv, d, block, L = 8, 2, 16, 8, 45
+    g = hq // hkv
+    q = rng.standard_normal((hq, d))
+    # float32 keys: the summaries hold float32 extrema, so every comparison is exact
+    k = (rng.standard_normal((hkv, L, d)) * np.exp(rng.standard_normal((hkv, 1, d)))).astype(np.float32)
+    k = k.astype(np.float64)
+    pre = Su.build_block_summaries(k, k, block)
+    got = S.quest_block_scores(q, pre["k_max"], pre["k_min"], g)
+    qm = q.reshape(hkv, g, d).mean(1)
+    for h in range(hkv):
+        for t in range(L):
+            assert float(qm[h] @ k[h, t]) <= got[h, t // block] + 1e-9
+    one = Su.build_block_summaries(k, k, 1)
+    got1 = S.quest_block_scores(q, one["k_max"], one["k_min"], g)
+    np.testing.assert_allclose(got1, np.einsum("hd,htd->ht", qm, k), rtol=1e-12, atol=1e-12)
+    qp = np.abs(q)
+    np.testing.assert_allclose(S.quest_block_scores(qp, pre["k_max"], pre["k_min"], g),
+                               np.einsum("hd,hbd->hb", qp.reshape(hkv, g, d).mean(1), pre["k_max"]), rtol=1e-6)
+    np.testing.assert_allclose(S.quest_block_scores(-qp, pre["k_max"], pre["k_min"], g),
+                               np.einsum("hd,hbd->hb", -qp.reshape(hkv, g, d).mean(1), pre["k_min"]), rtol=1e-6)
+    kx = pre["k_max"].copy()
+    kx[:, 2] = -np.inf
+    assert np.all(S.quest_block_scores(q, kx, pre["k_min"], g)[:, 2] == -np.inf)
+
+
 def _brute_topk(scores, nb, k, ff, fl, in_k):
     forced = sorted(set(range(min(ff, nb))) | set(range(max(nb - fl, 0), nb)))
     keff = k - len(forced) if in_k else k
@@ -341,3 +373,39 @@ def test_case_generator_is_reproducible():
     assert np.array_equal(a["pool_k"], b["pool_k"]) and np.array_equal(a["block_table"], b["block_table"])
     for i, L in enumerate([40, 17]):
         assert np.array_equal(P.paged_gather(a["pool_k"], a["block_table"][i], L, 16), a["k"][i])
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_torch_path_matches_numpy_oracle(fp8):
+    """The timed torch CPU restatement (oracle.torch_path) equals the numpy oracle:
+    same chosen blocks (mean-key and Quest scores), outputs within float32 rounding."""
+    from oracle import torch_path as T
+
+    hq, hkv, d, page, block, k = 16, 4, 32, 16, 32, 3
+    lens = [200, 77]
+    case = make_case(seed=11, batch=2, hq=hq, hkv=hkv, d=d, seq_lens=lens, page_size=page, k_outlier=True,
+                     fp8=fp8)
+    if fp8:
+        pk = torch.from_numpy(case["pool_k_codes"]).view(torch.float8_e4m3fn)
+        pv = torch.from_numpy(case["pool_v_codes"]).view(torch.float8_e4m3fn)
+        scales = (torch.from_numpy(case["k_scale"]), torch.from_numpy(case["v_scale"]))
+    else:
+        pk, pv, scales = torch.from_numpy(case["pool_k"]), torch.from_numpy(case["pool_v"]), None
+    table = torch.from_numpy(case["block_table"])
+    for b, L in enumerate(lens):
+        pre = Su.build_block_summaries(case["k"][b], case["v"][b], block)
+        nb = pre["block_valid_counts"].shape[0]
+        for mode in ("mean", "quest"):
+            if mode == "mean":
+                ref_sc = S.topk_block_scores(case["q"][b], pre["k_bar"], pre["block_valid_counts"], hq // hkv)
+                kb = torch.from_numpy(pre["k_bar"])
+            else:
+                ref_sc = S.quest_block_scores(case["q"][b], pre["k_max"], pre["k_min"], hq // hkv)
+                kb = (torch.from_numpy(pre["k_max"]), torch.from_numpy(pre["k_min"]))
+            out, chosen = T.topk_layer_call(torch.from_numpy(case["q"][b]), pk, pv, table[b], L, kb, block=block,
+                                            page=page, k=k, forced_last=1, scales=scales, score_mode=mode)
+            ref_idx = [S.select_topk(ref_sc[h], nb, k, 0, 1, False) for h in range(hkv)]
+            for h in range(hkv):
+                assert np.array_equal(chosen[h].numpy(), ref_idx[h]), (b, mode, h)
+            ref = A.sparse_decode(case["q"][b], case["k"][b], case["v"][b], ref_idx, block)
+            np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)

@@ -15,6 +15,7 @@ import math
 import os
 
 import torch
+import torch.nn.functional as F
 
 from . import _native as N
 from .ops import _code, _require_cuda, _stream, workspace_tensor
@@ -25,23 +26,24 @@ SELECT_CHUNK = 16  # blocks per selection-stats partial (CBT/core.py:27)
 # ------------------------------------------------------------------ layout and summaries
 
 def _pad_blocks(x, block_size):
-    """``[Hkv, P, ...] -> ([Hkv, nb, B, ...], nb)``, zero-padding the last block
-    (CBT/core.py:383-395): a view when ``P`` is a multiple of ``B``."""
-    n_heads, seq_len = x.shape[:2]
-    n_blocks = math.ceil(seq_len / block_size)
-    pad_len = n_blocks * block_size - seq_len
-    if pad_len > 0:
-        pad = torch.zeros((n_heads, pad_len, *x.shape[2:]), device=x.device, dtype=x.dtype)
-        x = torch.cat([x, pad], dim=1)
-    return x.reshape(n_heads, n_blocks, block_size, *x.shape[2:]), n_blocks
+    """``[Hkv, P, *rest] -> ([Hkv, nb, B, *rest], nb)``: the prompt cut into blocks of
+    ``block_size`` tokens with the last one zero-filled (CBT/core.py:383-395).  A view
+    (no copy) when ``P`` is a multiple of the block size."""
+    seq_len = int(x.shape[1])
+    n_blocks = -(-seq_len // block_size)
+    short = n_blocks * block_size - seq_len
+    if short:
+        # F.pad lists the trailing dims first: leave them, extend dim 1 at its end
+        x = F.pad(x, (0, 0) * (x.dim() - 2) + (0, short))
+    return x.unflatten(1, (n_blocks, block_size)), n_blocks
 
 
 def _ensure_paged_layout(x, block_size):
-    """Keep ``[Hkv, nb, B, D]`` addressable as head stride + token rows (CBT/core.py:397-408)."""
-    head_dim = int(x.shape[-1])
-    if x.stride(3) == 1 and x.stride(2) == head_dim and x.stride(1) == block_size * head_dim:
-        return x
-    return x.contiguous()
+    """The kernels address a ``[Hkv, nb, B, D]`` view by its head stride plus row-major
+    (block, token, dim) offsets, so cache slices are used in place; any other layout
+    is copied once (CBT/core.py:397-408)."""
+    row_major = (block_size * int(x.shape[-1]), int(x.shape[-1]), 1)
+    return x if tuple(x.stride()[1:]) == row_major else x.contiguous()
 
 
 def summary_storage_dtypes(source_dtype, *, summary_dtype=None, mixed=None, k_bar_dtype=None):
@@ -354,21 +356,24 @@ def fixed_mask_hybrid_attention(*, q_grouped, prompt_prefix, selected, k_suffix,
 
 
 def _condition_stats(*, selected, size, cluster_exists, prompt_len, suffix_len):
-    """Lazy device-side routing statistics (CBT/core.py:1441-1456)."""
-    n_kv_heads, group_size, n_query = selected.shape[:3]
-    size_view = size.view(1, 1, n_query, -1)
-    selected_tokens = (selected.long() * size_view).sum()
-    cluster_active = (~selected) & cluster_exists.view(1, 1, n_query, -1)
-    suffix_tokens = int(max(int(suffix_len), 0) * n_kv_heads * group_size)
-    n_rows = int(n_kv_heads * group_size * n_query)
-    total_available = int((int(prompt_len) + max(int(suffix_len), 0)) * n_rows)
+    """Routing statistics of one decode step (CBT/core.py:1441-1456), left on the
+    device: each query row attends its selected blocks' tokens, one representative
+    per unselected existing block and the exact suffix.  ``selected [Hkv, G, 1, nb]``
+    (the fused call's selection output), ``size [1, nb]`` valid tokens per block."""
+    picks = selected.reshape(-1, selected.shape[-1])          # [query rows, nb]
+    n_rows = int(picks.shape[0])
+    tokens = size.reshape(1, -1).long()
+    exists = cluster_exists.reshape(1, -1)
+    sfx = max(int(suffix_len), 0)
+    picked_tokens = torch.where(picks, tokens, 0).sum()
+    representatives = (exists & ~picks).sum()
     return {
         "rows": n_rows,
-        "clusters": cluster_exists.sum() * n_kv_heads * group_size,
-        "selected_clusters": selected.sum(),
-        "selected_tokens": selected_tokens,
-        "hybrid_tokens": selected_tokens + cluster_active.sum() + suffix_tokens,
-        "total_available": total_available,
+        "clusters": exists.sum() * n_rows,
+        "selected_clusters": picks.sum(),
+        "selected_tokens": picked_tokens,
+        "hybrid_tokens": picked_tokens + representatives + sfx * n_rows,
+        "total_available": (int(prompt_len) + sfx) * n_rows,
     }
 
 
@@ -396,9 +401,11 @@ def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scal
     ``query [B, Hq, L, D]``, ``key/value [B, Hkv, T, D]`` -> ``([B, L, Hq, D], None)``.
     Single-token decode (L == 1) runs the HIP dense paged decode; the keys it reads
     are ``[0, n_b)`` with ``n_b`` the number of positions ``attention_mask`` allows
-    for the query (all T when no mask is given), so the allowed keys must be a
-    prefix (causal decode without left padding).  Multi-token calls (prompt prefill)
-    go to transformers' SDPA attention function, as in the reference."""
+    for the query (all T when no mask is given).  A mask whose allowed keys are not
+    such a prefix (left-padded batches) is detected on the host and goes to torch
+    SDPA with the mask; multi-token calls (prompt prefill) go to transformers' SDPA
+    attention function, as in the reference.  Under graph capture the mask must be
+    None."""
     if query.shape[2] != 1:
         from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
@@ -417,7 +424,19 @@ def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scal
     else:
         m = attention_mask[:, 0, -1, :t_len] if attention_mask.dim() == 4 else attention_mask[:, -1, :t_len]
         allowed = m if m.dtype == torch.bool else m > torch.finfo(m.dtype).min / 2
-        seq = allowed.sum(-1).to(torch.int32).expand(bsz).contiguous()
+        allowed = allowed.expand(bsz, t_len)
+        seq = allowed.sum(-1).to(torch.int32).contiguous()
+        # the kernel attends keys [0, n): a mask that is not such a prefix (left
+        # padding) goes to transformers' SDPA attention, as the reference's does
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("decode under graph capture takes attention_mask=None (keys [0, T) attended)")
+        prefix = torch.arange(t_len, device=allowed.device)[None, :] < seq[:, None]
+        if not bool(torch.equal(prefix, allowed)):
+            mask = attention_mask[..., :t_len] if attention_mask.dim() == 4 else attention_mask[:, None, :, :t_len]
+            mask = mask if mask.dtype == torch.bool else mask.to(query.dtype)
+            out = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,
+                                                 enable_gqa=hq != hkv)
+            return out.transpose(1, 2).contiguous(), None
     # each sequence is one page of ceil16(T) tokens: page b = batch entry b; the
     # kernel never reads a token at or past seq_len, so the padding is never touched
     kv = N.PagedKV()

@@ -1,17 +1,31 @@
-"""Decode-loop integration: the reference's HF attention hook, its runner and its
-generation loops (eager, and one graph replay per token) over the HIP kernels.
+"""Decode-loop integration: the HF attention hook of the condition-block decode and
+greedy generation over it (eager, and one graph replay per token).
 
-Mirrors, with the same names, arguments, environment switches and ``ValueError``
-contract, ``llama/script/analysis/condition_block_gen/methods/condition_block_triton_impl/core.py``
-(``CBT/core.py``): ``generate_condition_block_cached`` (:60-186),
-``_generate_condition_block_cuda_graph`` (:189-314), ``_static_cache_from_prefill``
-(:317-328), ``ConditionBlockDecodeRunner`` (:1203-1355), the attention contexts
-(:1358-1400), ``_sdpa_prefill_attention_forward`` (:1180-1200) and the lazy step
-statistics (:1403-1530, ``CBG/methods/patching.py:69-95``).  Single-token decode of
-every compressed layer runs the fused condition path of
-``interattn_amd.condition_block``; uncompressed layers run the HIP dense decode;
-prompt prefill stays on torch SDPA exactly as in the reference.  On ROCm
-``torch.cuda.CUDAGraph`` records a HIP graph.
+The public names, their arguments, the environment switches
+(``CONDITION_BLOCK_SKIP_STATS``, ``CONDITION_BLOCK_CUDA_GRAPH``,
+``CONDITION_BLOCK_STATIC_CACHE``, ``CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE``) and
+the ``ValueError`` texts are the reference's interface
+(``llama/script/analysis/condition_block_gen/methods/condition_block_triton_impl/core.py``,
+``CBT/core.py`` below: the loops :60-330, the runner :1203-1355, the contexts
+:1358-1400, the statistics helpers :1403-1530 and ``CBG/methods/patching.py:69-95``),
+so the reference's decode driver can call this module in its place.
+
+How it is built here:
+
+* one ``_GreedyStep`` object owns the per-token device state (next input id,
+  cache position, output slot, the runner's suffix length) and runs one decode
+  step; the eager loop calls it token by token, the graph loop captures it once and
+  replays it;
+* the prompt K/V reach a ``StaticCache`` through the cache's own ``update`` (so its
+  length counter is right for the decode steps that follow);
+* routing statistics stay on the device during generation (the runner takes them
+  from the fused call's selection output) and are read back in one transfer when
+  generation ends;
+* the four attention contexts share one attribute-swapping context manager.
+
+Single-token decode of a compressed layer runs ``condition_block``'s fused HIP
+path; other decode layers run the HIP dense decode; prompt prefill stays on torch
+SDPA as in the reference.  On ROCm ``torch.cuda.CUDAGraph`` records a HIP graph.
 """
 
 import contextlib
@@ -34,6 +48,12 @@ __all__ = [
     "summarize_condition_block_step_metadata",
 ]
 
+_SKIP_STATS = "CONDITION_BLOCK_SKIP_STATS"
+
+
+def _env_on(name):
+    return os.environ.get(name) == "1"
+
 
 def _modeling_llama():
     from transformers.models.llama import modeling_llama
@@ -41,167 +61,150 @@ def _modeling_llama():
     return modeling_llama
 
 
-# ------------------------------------------------------------------ step statistics
+# ------------------------------------------------------------------ routing statistics
+
+def _with_means(stats):
+    """``stats`` plus its derived ratios: hybrid tokens per query row, and per visible
+    token (the causal and visible budgets coincide for a decode step)."""
+    hybrid = float(int(stats.get("hybrid_tokens", 0)))
+    budget = hybrid / max(int(stats.get("total_available", 0)), 1)
+    return {**stats, "mean_hybrid_tokens": hybrid / max(int(stats.get("rows", 0)), 1),
+            "mean_budget_causal": budget, "mean_budget_visible": budget}
+
 
 def merge_stats(total, add):
-    """``CBG/methods/patching.py:69-71``."""
-    for key, value in add.items():
-        total[key] = int(total.get(key, 0)) + int(value)
+    """Add ``add``'s counts into ``total`` as Python ints (CBG/methods/patching.py:69)."""
+    total.update({key: int(total.get(key, 0)) + int(val) for key, val in add.items()})
 
 
 def summarize_stats(aggregate_stats, stats_by_layer):
-    """``CBG/methods/patching.py:74-95``."""
-    total_available = max(int(aggregate_stats.get("total_available", 0)), 1)
-    rows = max(int(aggregate_stats.get("rows", 0)), 1)
-    hybrid_tokens = int(aggregate_stats.get("hybrid_tokens", 0))
-    aggregate = {
-        **aggregate_stats,
-        "mean_hybrid_tokens": float(hybrid_tokens / rows),
-        "mean_budget_causal": float(hybrid_tokens / total_available),
-        "mean_budget_visible": float(hybrid_tokens / total_available),
-    }
-    by_layer = {}
-    for layer_idx, stats in stats_by_layer.items():
-        layer_total = max(int(stats.get("total_available", 0)), 1)
-        layer_rows = max(int(stats.get("rows", 0)), 1)
-        layer_hybrid = int(stats.get("hybrid_tokens", 0))
-        by_layer[layer_idx] = {
-            **stats,
-            "mean_hybrid_tokens": float(layer_hybrid / layer_rows),
-            "mean_budget_causal": float(layer_hybrid / layer_total),
-            "mean_budget_visible": float(layer_hybrid / layer_total),
-        }
-    return {"aggregate": aggregate, "by_layer": by_layer}
+    """Aggregate and per-layer statistics with their ratios (CBG/methods/patching.py:74)."""
+    return {"aggregate": _with_means(aggregate_stats),
+            "by_layer": {layer: _with_means(s) for layer, s in stats_by_layer.items()}}
 
 
 def full_attention_stats_for_heads(n_heads, pos_list):
-    """Routing statistics of a dense layer (CBT/core.py:1463-1472)."""
-    total_available = sum(int(pos) + 1 for pos in pos_list) * int(n_heads)
-    return {
-        "rows": int(n_heads) * len(pos_list),
-        "clusters": 0,
-        "selected_clusters": 0,
-        "selected_tokens": total_available,
-        "hybrid_tokens": total_available,
-        "total_available": total_available,
-    }
+    """Statistics of a dense layer (CBT/core.py:1463): every visible token is attended
+    by every query head."""
+    visible = int(n_heads) * sum(int(pos) + 1 for pos in pos_list)
+    return dict(rows=int(n_heads) * len(pos_list), clusters=0, selected_clusters=0, selected_tokens=visible,
+                hybrid_tokens=visible, total_available=visible)
 
 
 def _merge_stats_lazy(total, add):
-    for key, value in add.items():
-        total[key] = total[key] + value if key in total else value
-
-
-def _to_python_number(value):
-    if torch.is_tensor(value):
-        value = value.detach().cpu()
-        if value.numel() != 1:
-            raise ValueError("Expected scalar tensor in condition-block stats.")
-        return int(value.item())
-    return int(value)
-
-
-def _stats_ratio(numerator, denominator):
-    return float(_to_python_number(numerator) / max(_to_python_number(denominator), 1))
-
-
-def _materialize_stats(stats):
-    return {key: _to_python_number(value) for key, value in stats.items()}
+    """Add ``add`` into ``total`` without a host synchronisation (values may be device
+    tensors)."""
+    for key, val in add.items():
+        total[key] = val if key not in total else total[key] + val
 
 
 def _summarize_stats_lazy(aggregate_stats, stats_by_layer):
-    """Synchronisation-free per-step summary (CBT/core.py:1439-1447)."""
-    return {"aggregate": dict(aggregate_stats),
-            "by_layer": {int(i): dict(s) for i, s in stats_by_layer.items()}}
+    """Per-step snapshot of the runner's statistics (kept lazy: no device read)."""
+    return {"aggregate": dict(aggregate_stats), "by_layer": {int(k): dict(v) for k, v in stats_by_layer.items()}}
 
 
 def _full_generation_step_metadata(model, pos_list):
-    aggregate, by_layer = {}, {}
-    n_heads = int(model.config.num_attention_heads)
-    for layer_idx in range(int(model.config.num_hidden_layers)):
-        stats = full_attention_stats_for_heads(n_heads, pos_list)
-        by_layer[layer_idx] = stats
-        merge_stats(aggregate, stats)
+    n_layers, n_heads = int(model.config.num_hidden_layers), int(model.config.num_attention_heads)
+    by_layer = {i: full_attention_stats_for_heads(n_heads, pos_list) for i in range(n_layers)}
+    aggregate = {}
+    for s in by_layer.values():
+        merge_stats(aggregate, s)
     return summarize_stats(aggregate, by_layer)
 
 
+def _read_back(values):
+    """Python ints of a list of ints / one-element device tensors, with one transfer."""
+    tensors = [v for v in values if torch.is_tensor(v)]
+    if any(t.numel() != 1 for t in tensors):
+        raise ValueError("Expected scalar tensor in condition-block stats.")
+    host = iter(torch.stack([t.detach().reshape(()).to(torch.int64) for t in tensors]).tolist()) if tensors else None
+    return [int(next(host)) if torch.is_tensor(v) else int(v) for v in values]
+
+
 def summarize_condition_block_step_metadata(step_metadata):
-    """Materialise the per-step statistics after generation (CBT/core.py:1486-1530)."""
-    if os.environ.get("CONDITION_BLOCK_SKIP_STATS") == "1":
+    """Budget summary of a generation (CBT/core.py:1486): per-step equivalent budget
+    and the totals, read back from the device once."""
+    if _env_on(_SKIP_STATS):
         return {"condition_block_stats_disabled": True}
-    aggregate = {}
-    by_step = []
-    for step_idx, metadata in enumerate(step_metadata):
-        if not metadata:
-            continue
-        step_aggregate = metadata.get("aggregate", {})
-        by_step.append({"step": step_idx,
-                        "equiv_budget": _stats_ratio(step_aggregate.get("hybrid_tokens", 0),
-                                                     step_aggregate.get("total_available", 0))})
-        for key, value in step_aggregate.items():
-            if not key.startswith("mean_"):
-                _merge_stats_lazy(aggregate, {key: value})
-    materialized = _materialize_stats(aggregate)
-    total_available = max(int(materialized.get("total_available", 0)), 1)
-    rows = max(int(materialized.get("rows", 0)), 1)
-    hybrid_tokens = int(materialized.get("hybrid_tokens", 0))
-    equiv_budget = float(hybrid_tokens / total_available)
-    return {
-        "condition_block_equiv_budget": equiv_budget,
-        "condition_block_budget": {**materialized, "mean_hybrid_tokens": float(hybrid_tokens / rows),
-                                   "mean_budget_causal": equiv_budget, "mean_budget_visible": equiv_budget,
-                                   "by_step": by_step},
-    }
+    steps = [(i, m.get("aggregate", {})) for i, m in enumerate(step_metadata) if m]
+    totals = {}
+    for _, agg in steps:
+        _merge_stats_lazy(totals, {k: v for k, v in agg.items() if not k.startswith("mean_")})
+    # one transfer for every step's (hybrid, available) pair and every total
+    flat = [agg.get(k, 0) for _, agg in steps for k in ("hybrid_tokens", "total_available")]
+    keys = list(totals)
+    host = _read_back(flat + [totals[k] for k in keys])
+    pairs, tot = host[:len(flat)], dict(zip(keys, host[len(flat):]))
+    by_step = [{"step": i, "equiv_budget": float(pairs[2 * n] / max(pairs[2 * n + 1], 1))}
+               for n, (i, _) in enumerate(steps)]
+    summary = _with_means(tot)
+    return {"condition_block_equiv_budget": summary["mean_budget_causal"],
+            "condition_block_budget": {**summary, "by_step": by_step}}
 
 
 # ------------------------------------------------------------------ attention functions
 
 def _sdpa_prefill_attention_forward(module, query, key, value, attention_mask, scaling, dropout=0.0, **_kwargs):
-    """Causal prompt prefill on torch SDPA (CBT/core.py:1180-1200)."""
-    attn_output = F.scaled_dot_product_attention(
-        query, key, value, attn_mask=None, dropout_p=float(dropout) if module.training else 0.0, is_causal=True,
-        scale=scaling, enable_gqa=query.shape[1] != key.shape[1])
-    return attn_output.transpose(1, 2).contiguous(), None
+    """Causal prompt prefill on torch SDPA (CBT/core.py:1180): ``[B, Hq, L, D]`` in,
+    ``([B, L, Hq, D], None)`` out; grouped-query heads are expanded by SDPA."""
+    p_drop = float(dropout) if module.training else 0.0
+    out = F.scaled_dot_product_attention(query, key, value, dropout_p=p_drop, is_causal=True, scale=scaling,
+                                         enable_gqa=query.shape[1] != key.shape[1])
+    return out.transpose(1, 2).contiguous(), None
 
 
 class ConditionBlockDecodeRunner:
-    """The HF attention hook of the condition-block decode (CBT/core.py:1203-1355):
-    builds each layer's prompt summaries on its first decode step, then routes every
-    single-token decode of a compressed layer through the fused HIP path."""
+    """The HF attention hook of the condition-block decode (CBT/core.py:1203-1355).
+
+    Per call: prompt prefill (``q_len > 1``) goes to SDPA; a decode step of a layer
+    outside ``layer_idx_list`` or below ``full_attention_layers`` goes to the HIP
+    dense decode; any other decode step builds (once per layer) the layer's prompt
+    summaries and runs the fused HIP condition path over the prompt blocks plus the
+    exact suffix of generated tokens.  The suffix length is read by the kernels from
+    ``suffix_len_dev``: ``reset_step`` writes it in the eager loop, the graph loop
+    advances it on the device.  With ``static_suffix`` the hook passes the whole
+    static-cache rows, so every shape is the same at every step."""
 
     def __init__(self, *, model, model_config, layer_idx_list, full_attention_layers, block_size, eps, prompt_len,
                  pos, prompt_prefix_cache, term1_mass_exp=False):
         self.model_config = model_config
-        self.module_to_layer_idx = {id(layer.self_attn): int(i) for i, layer in enumerate(model.model.layers)}
-        self.layer_idx_set = {int(i) for i in layer_idx_list}
+        self.module_to_layer_idx = {id(layer.self_attn): i for i, layer in enumerate(model.model.layers)}
+        self.layer_idx_set = set(map(int, layer_idx_list))
         self.full_attention_layers = int(full_attention_layers)
-        self.block_size = int(block_size)
-        self.eps = float(eps)
-        self.prompt_len = int(prompt_len)
-        self.pos = int(pos)
+        self.block_size, self.eps = int(block_size), float(eps)
+        self.prompt_len, self.pos = int(prompt_len), int(pos)
         self.prompt_prefix_cache = prompt_prefix_cache
         self.term1_mass_exp = bool(term1_mass_exp)
         self.workspace_by_layer = {}
-        self.stats_by_layer = {}
-        self.aggregate_stats = {}
-        self.skip_stats = os.environ.get("CONDITION_BLOCK_SKIP_STATS") == "1"
-        # suffix length read by the fused decode on the device: refreshed by
-        # reset_step() in the eager loop, advanced inside the graph otherwise
+        self.stats_by_layer, self.aggregate_stats = {}, {}
+        self.skip_stats = _env_on(_SKIP_STATS)
         self.suffix_len_dev = torch.zeros((), dtype=torch.int32, device=next(model.parameters()).device)
-        # full static-cache views + suffix_len_dev keep every shape step-invariant
         self.static_suffix = False
 
     def should_compress(self, layer_idx):
-        return int(layer_idx) in self.layer_idx_set and int(layer_idx) >= self.full_attention_layers
+        return int(layer_idx) >= self.full_attention_layers and int(layer_idx) in self.layer_idx_set
 
     def summarize(self):
         return _summarize_stats_lazy(self.aggregate_stats, self.stats_by_layer)
 
     def reset_step(self, pos):
+        """Start decode position ``pos``: the suffix holds the generated tokens up to it."""
         self.pos = int(pos)
-        self.suffix_len_dev.fill_(max(self.pos + 1 - self.prompt_len, 0))
+        self.suffix_len_dev.fill_(max(0, self.pos + 1 - self.prompt_len))
         self.stats_by_layer.clear()
         self.aggregate_stats.clear()
+
+    def _record(self, layer_idx, stats):
+        self.stats_by_layer[int(layer_idx)] = stats
+        _merge_stats_lazy(self.aggregate_stats, stats)
+
+    def _prefix(self, layer_idx, k_rows, v_rows):
+        """Prompt summaries of one layer, built on its first decode step and kept."""
+        key = (int(layer_idx), self.prompt_len, self.block_size)
+        if key not in self.prompt_prefix_cache:
+            p = self.prompt_len
+            self.prompt_prefix_cache[key] = _build_prompt_blocks(k_rows[:, :p], v_rows[:, :p], self.block_size)
+        return self.prompt_prefix_cache[key]
 
     def hybrid_attention_forward(self, module, query, key, value, attention_mask, scaling, dropout=0.0, **kwargs):
         layer_idx = getattr(module, "layer_idx", None)
@@ -211,43 +214,37 @@ class ConditionBlockDecodeRunner:
             return _sdpa_prefill_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
                                                    dropout=dropout, **kwargs)
         if layer_idx is None or not self.should_compress(layer_idx):
-            if layer_idx in self.layer_idx_set and not self.skip_stats:
-                stats = full_attention_stats_for_heads(query.shape[1], [self.pos])
-                self.stats_by_layer[int(layer_idx)] = stats
-                _merge_stats_lazy(self.aggregate_stats, stats)
+            if not self.skip_stats and layer_idx in self.layer_idx_set:
+                self._record(layer_idx, full_attention_stats_for_heads(query.shape[1], [self.pos]))
             return _sdpa_full_attention_forward(module, query, key, value, attention_mask, scaling=scaling,
                                                 dropout=dropout, **kwargs)
-        if query.shape[0] != 1 or query.shape[2] != 1:
+        return self._sparse_decode(int(layer_idx), query, key, value)
+
+    def _sparse_decode(self, layer_idx, query, key, value):
+        batch, n_heads, q_len, head_dim = query.shape
+        if batch != 1 or q_len != 1:
             raise ValueError("condition_block fast path expects batch_size=1 and q_len=1.")
         if self.pos < self.prompt_len:
             raise ValueError("condition_block fast path expects generated-token decode positions.")
-        _batch, n_heads, q_len, head_dim = query.shape
         n_kv_heads = int(key.shape[1])
-        if n_heads % n_kv_heads != 0:
+        if n_heads % n_kv_heads:
             raise ValueError("condition_block fast path expects grouped query attention.")
-        q_grouped = query[0].reshape(n_kv_heads, n_heads // n_kv_heads, q_len, head_dim)
-        if self.static_suffix:
-            k_all, v_all = key[0], value[0]
-        else:
-            k_all = key[0, :, :self.pos + 1]
-            v_all = value[0, :, :self.pos + 1]
-        cache_key = (int(layer_idx), self.prompt_len, self.block_size)
-        prompt_prefix = self.prompt_prefix_cache.get(cache_key)
-        if prompt_prefix is None:
-            prompt_prefix = _build_prompt_blocks(k_all[:, :self.prompt_len], v_all[:, :self.prompt_len],
-                                                 self.block_size)
-            self.prompt_prefix_cache[cache_key] = prompt_prefix
-        output, stats = _condition_block_decode_output(
-            q_grouped=q_grouped, prompt_prefix=prompt_prefix, k_suffix=k_all[:, self.prompt_len:],
-            v_suffix=v_all[:, self.prompt_len:], suffix_len_dev=self.suffix_len_dev, block_size=self.block_size,
-            eps=self.eps, prompt_len=self.prompt_len, attention_dtype=query.dtype,
-            workspace=self.workspace_by_layer.setdefault(int(layer_idx), {}), term1_mass_exp=self.term1_mass_exp,
+        # rows of the cache this step may read: the whole static cache (validity from
+        # suffix_len_dev), else the visible prefix
+        visible = key.shape[2] if self.static_suffix else self.pos + 1
+        k_rows, v_rows = key[0, :, :visible], value[0, :, :visible]
+        prefix = self._prefix(layer_idx, k_rows, v_rows)
+        out, stats = _condition_block_decode_output(
+            q_grouped=query[0].view(n_kv_heads, n_heads // n_kv_heads, 1, head_dim), prompt_prefix=prefix,
+            k_suffix=k_rows[:, self.prompt_len:], v_suffix=v_rows[:, self.prompt_len:],
+            suffix_len_dev=self.suffix_len_dev, block_size=self.block_size, eps=self.eps,
+            prompt_len=self.prompt_len, attention_dtype=query.dtype,
+            workspace=self.workspace_by_layer.setdefault(layer_idx, {}), term1_mass_exp=self.term1_mass_exp,
             collect_stats=not self.skip_stats)
-        output = output.reshape(n_heads, q_len, head_dim).permute(1, 0, 2).unsqueeze(0)
         if stats is not None:
-            self.stats_by_layer[int(layer_idx)] = stats
-            _merge_stats_lazy(self.aggregate_stats, stats)
-        return output.to(query.dtype), None
+            self._record(layer_idx, stats)
+        # [Hkv, G, 1, D] -> the HF layout [1, q_len, Hq, D]
+        return out.reshape(1, 1, n_heads, head_dim).to(query.dtype), None
 
 
 class PagedTopkDecodeRunner:
@@ -357,52 +354,41 @@ class PagedTopkDecodeRunner:
 # ------------------------------------------------------------------ contexts
 
 @contextlib.contextmanager
-def _no_causal_mask_context():
-    """Skip HF causal-mask construction in the graphed step (CBT/core.py:1358-1370)."""
-    ml = _modeling_llama()
-    original = ml.create_causal_mask
-    ml.create_causal_mask = lambda *args, **kwargs: None
+def _swapped(owner, name, value):
+    """Temporarily replace ``owner.name`` with ``value``."""
+    saved = getattr(owner, name)
+    setattr(owner, name, value)
     try:
         yield
     finally:
-        ml.create_causal_mask = original
+        setattr(owner, name, saved)
+
+
+def _no_causal_mask_context():
+    """No HF causal-mask construction during the graphed step (CBT/core.py:1358): the
+    sparse layers ignore the mask, and building it copies a host scalar to the device,
+    which graph capture forbids."""
+    return _swapped(_modeling_llama(), "create_causal_mask", lambda *args, **kwargs: None)
 
 
 @contextlib.contextmanager
 def condition_block_decode_context(runner):
-    """Install ``runner.hybrid_attention_forward`` as HF's eager attention (CBT/core.py:1373-1380)."""
-    ml = _modeling_llama()
-    original = ml.eager_attention_forward
-    ml.eager_attention_forward = runner.hybrid_attention_forward
-    try:
+    """Route HF's eager attention through ``runner`` (CBT/core.py:1373)."""
+    with _swapped(_modeling_llama(), "eager_attention_forward", runner.hybrid_attention_forward):
         yield runner
-    finally:
-        ml.eager_attention_forward = original
 
 
-@contextlib.contextmanager
 def full_attention_sdpa_context():
-    """Every decode on the HIP dense path (CBT/core.py:1383-1390)."""
-    ml = _modeling_llama()
-    original = ml.eager_attention_forward
-    ml.eager_attention_forward = _sdpa_full_attention_forward
-    try:
-        yield
-    finally:
-        ml.eager_attention_forward = original
+    """Every decode on the HIP dense path (CBT/core.py:1383)."""
+    return _swapped(_modeling_llama(), "eager_attention_forward", _sdpa_full_attention_forward)
 
 
-@contextlib.contextmanager
 def model_attention_implementation(model, implementation):
-    original = model.config._attn_implementation
-    model.config._attn_implementation = implementation
-    try:
-        yield
-    finally:
-        model.config._attn_implementation = original
+    """Run the model under another HF attention implementation (CBT/core.py:1393)."""
+    return _swapped(model.config, "_attn_implementation", implementation)
 
 
-# ------------------------------------------------------------------ generation loops
+# ------------------------------------------------------------------ generation
 
 def run_prefill_only_condition_block(**_kwargs):
     raise RuntimeError("condition_block now uses the cached generate path only. "
@@ -416,185 +402,162 @@ def build_condition_args(method, prompt_len):
 
 
 def _stop_token_ids(tokenizer, dataset):
-    ids = []
-    if tokenizer is not None and tokenizer.eos_token_id is not None:
-        ids.append(int(tokenizer.eos_token_id))
-    if tokenizer is not None and dataset == "samsum":
-        newline_ids = tokenizer.encode("\n", add_special_tokens=False)
-        if newline_ids:
-            ids.append(int(newline_ids[-1]))
+    """EOS, plus the newline token for samsum (its answers are one line)."""
+    if tokenizer is None:
+        return []
+    ids = [] if tokenizer.eos_token_id is None else [int(tokenizer.eos_token_id)]
+    if dataset == "samsum":
+        ids += [int(t) for t in tokenizer.encode("\n", add_special_tokens=False)[-1:]]
     return ids
 
 
-def _should_stop(next_id, stop_ids_tensor):
-    if stop_ids_tensor is None:
-        return False
-    return bool(torch.isin(next_id, stop_ids_tensor).all().item())
-
-
 def _static_cache_from_prefill(config, prefill_cache, max_cache_len):
-    """Move the prefill KV into a StaticCache of ``max_cache_len`` (CBT/core.py:317-328)."""
+    """A ``StaticCache`` of ``max_cache_len`` holding the prefill's K/V (CBT/core.py:317):
+    written through the cache's ``update`` so that its length counter points past the
+    prompt and the first decode step writes right after it."""
     from transformers import StaticCache
 
-    static_cache = StaticCache(config=config, max_cache_len=int(max_cache_len))
-    for layer_idx, source_layer in enumerate(prefill_cache.layers):
-        key_states, value_states = source_layer.keys, source_layer.values
-        target = static_cache.layers[layer_idx]
-        target.lazy_initialization(key_states[:, :, :1], value_states[:, :, :1])
-        seq_len = int(key_states.shape[2])
-        target.keys[:, :, :seq_len].copy_(key_states)
-        target.values[:, :, :seq_len].copy_(value_states)
-    return static_cache
+    static = StaticCache(config=config, max_cache_len=int(max_cache_len))
+    for i, layer in enumerate(prefill_cache.layers):
+        static.update(layer.keys, layer.values, i)
+    return static
+
+
+def _prefill(model, input_ids, attention_mask, past_key_values=None):
+    """Prompt forward on torch SDPA; returns (first greedy token [1, 1], KV cache)."""
+    with model_attention_implementation(model, "sdpa"), torch.no_grad():
+        out = model(input_ids=input_ids, attention_mask=attention_mask, past_key_values=past_key_values,
+                    use_cache=True, logits_to_keep=1)
+    return out.logits[:, -1].float().argmax(-1, keepdim=True), out.past_key_values
+
+
+class _GreedyStep:
+    """Device state of greedy decoding and one decode step over it.
+
+    ``tokens[i]`` receives generated token ``i``; the step feeds ``step_ids`` at
+    ``cache_pos``, writes the argmax at ``tokens[slot]`` and advances the input, the
+    position, the slot and (graph mode) the runner's suffix length, all on the
+    device, so one step can be captured and replayed.  The eager loop runs the same
+    step and additionally grows the attention mask on the host."""
+
+    def __init__(self, model, runner, cache, first, prompt_len, n_new, *, mask=None, advance_suffix=False):
+        dev = first.device
+        self.model, self.runner, self.cache = model, runner, cache
+        self.tokens = torch.zeros(n_new, dtype=first.dtype, device=dev)
+        self.tokens[:1] = first.view(1)
+        self.step_ids = first.view(1, 1).clone()
+        self.cache_pos = torch.full((1,), int(prompt_len), dtype=torch.long, device=dev)
+        self.slot = torch.ones(1, dtype=torch.long, device=dev)
+        self.mask = mask
+        self.advance_suffix = advance_suffix
+
+    def __call__(self):
+        out = self.model(input_ids=self.step_ids, attention_mask=self.mask, past_key_values=self.cache,
+                         use_cache=True, logits_to_keep=1, cache_position=self.cache_pos)
+        nxt = out.logits[0, -1].float().argmax(-1).view(1)
+        self.tokens.index_copy_(0, self.slot, nxt)
+        self.step_ids.copy_(nxt.view(1, 1))
+        self.cache_pos.add_(1)
+        self.slot.add_(1)
+        if self.advance_suffix:
+            self.runner.suffix_len_dev.add_(1)
+        self.cache = out.past_key_values
+        return nxt
+
+
+def _runner_for(model, method, prompt_len, pos, term1_mass_exp):
+    return ConditionBlockDecodeRunner(
+        model=model, model_config=model.config, layer_idx_list=range(int(model.config.num_hidden_layers)),
+        full_attention_layers=method.full_attention_layers, block_size=method.condition_block_size,
+        eps=method.condition_eps, prompt_len=prompt_len, pos=pos, prompt_prefix_cache={},
+        term1_mass_exp=term1_mass_exp)
 
 
 def generate_condition_block_cached(*, model, tokenizer, input_ids, attention_mask, method, device, dataset=None,
                                     term1_mass_exp=False):
-    """Greedy generation with SDPA prefill and condition-block decode (CBT/core.py:60-186).
-    ``method`` carries ``condition_delta_mode, condition_block_size, condition_eps,
-    full_attention_layers, max_new_tokens``.  Returns ``(output_ids [1, n], metadata)``."""
+    """Greedy generation: SDPA prefill, then condition-block decode one token at a
+    time (CBT/core.py:60-186), stopping at a stop token.  ``method`` carries
+    ``condition_delta_mode, condition_block_size, condition_eps,
+    full_attention_layers, max_new_tokens``.  Returns ``(output_ids [1, n], metadata)``;
+    with ``CONDITION_BLOCK_CUDA_GRAPH=1`` the graph-replay loop runs instead."""
     if method.condition_delta_mode != "range_bound":
         raise ValueError("condition_block only supports delta_mode='range_bound'.")
     if int(input_ids.shape[0]) != 1:
         raise ValueError("condition_block generate currently expects batch_size=1.")
-    if os.environ.get("CONDITION_BLOCK_CUDA_GRAPH") == "1":
+    if _env_on("CONDITION_BLOCK_CUDA_GRAPH"):
         return _generate_condition_block_cuda_graph(model=model, tokenizer=tokenizer, input_ids=input_ids,
                                                     attention_mask=attention_mask, method=method, dataset=dataset,
                                                     term1_mass_exp=term1_mass_exp)
-    from transformers import StaticCache
+    prompt_len, n_new = int(input_ids.shape[1]), int(method.max_new_tokens)
+    if n_new <= 0:
+        return input_ids.new_empty((1, 0)), summarize_condition_block_step_metadata([])
+    stop_ids = torch.tensor(_stop_token_ids(tokenizer, dataset), device=input_ids.device, dtype=input_ids.dtype)
+    cache = None
+    if _env_on("CONDITION_BLOCK_STATIC_CACHE"):
+        from transformers import StaticCache
 
-    prompt_len = int(input_ids.shape[1])
-    max_new_tokens = int(method.max_new_tokens)
-    if max_new_tokens <= 0:
-        return (torch.empty((1, 0), device=input_ids.device, dtype=input_ids.dtype),
-                summarize_condition_block_step_metadata([]))
-    stop_token_ids = _stop_token_ids(tokenizer, dataset)
-    stop_ids_tensor = (torch.tensor(stop_token_ids, device=input_ids.device, dtype=input_ids.dtype)
-                       if stop_token_ids else None)
-    layer_idx_list = list(range(int(model.config.num_hidden_layers)))
-    prompt_prefix_cache = {}
-    generated, step_metadata = [], []
-    collect_stats = os.environ.get("CONDITION_BLOCK_SKIP_STATS") != "1"
-    cur_mask = attention_mask
-    total_len = prompt_len
-    past_key_values = None
-    if os.environ.get("CONDITION_BLOCK_STATIC_CACHE") == "1":
-        past_key_values = StaticCache(config=model.config, max_cache_len=prompt_len + max_new_tokens)
-    with model_attention_implementation(model, "sdpa"), torch.no_grad():
-        outputs = model(input_ids=input_ids, attention_mask=cur_mask, past_key_values=past_key_values,
-                        use_cache=True, logits_to_keep=1)
-    logits = outputs.logits.float()
-    past_key_values = outputs.past_key_values
-    if os.environ.get("CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE") == "1":
-        past_key_values = _static_cache_from_prefill(model.config, past_key_values,
-                                                     max_cache_len=prompt_len + max_new_tokens)
-    if collect_stats:
-        step_metadata.append(_full_generation_step_metadata(model, [total_len - 1]))
-    next_id = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
-    generated.append(next_id)
-    if _should_stop(next_id, stop_ids_tensor):
-        return torch.cat(generated, dim=1), summarize_condition_block_step_metadata(step_metadata)
-    cur_mask = torch.cat([cur_mask, torch.ones_like(next_id)], dim=1)
-    step_input_ids = next_id
-    total_len += 1
-    runner = ConditionBlockDecodeRunner(model=model, model_config=model.config, layer_idx_list=layer_idx_list,
-                                        full_attention_layers=method.full_attention_layers,
-                                        block_size=method.condition_block_size, eps=method.condition_eps,
-                                        prompt_len=prompt_len, pos=total_len - 1,
-                                        prompt_prefix_cache=prompt_prefix_cache, term1_mass_exp=term1_mass_exp)
-    with condition_block_decode_context(runner):
-        for _step in range(1, max_new_tokens):
-            runner.reset_step(total_len - 1)
-            with torch.no_grad():
-                cache_position = None
-                if os.environ.get("CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE") == "1":
-                    cache_position = torch.tensor([total_len - 1], device=input_ids.device, dtype=torch.long)
-                outputs = model(input_ids=step_input_ids, attention_mask=cur_mask, past_key_values=past_key_values,
-                                use_cache=True, logits_to_keep=1, cache_position=cache_position)
-            logits = outputs.logits.float()
-            past_key_values = outputs.past_key_values
-            if collect_stats:
-                step_metadata.append(runner.summarize())
-            next_id = torch.argmax(logits[:, -1, :], dim=-1, keepdim=True)
-            generated.append(next_id)
-            if _should_stop(next_id, stop_ids_tensor):
-                break
-            cur_mask = torch.cat([cur_mask, torch.ones_like(next_id)], dim=1)
-            step_input_ids = next_id
-            total_len += 1
-    return torch.cat(generated, dim=1), summarize_condition_block_step_metadata(step_metadata)
+        cache = StaticCache(config=model.config, max_cache_len=prompt_len + n_new)
+    first, cache = _prefill(model, input_ids, attention_mask, cache)
+    if _env_on("CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE"):
+        cache = _static_cache_from_prefill(model.config, cache, prompt_len + n_new)
+    collect = not _env_on(_SKIP_STATS)
+    metadata = [_full_generation_step_metadata(model, [prompt_len - 1])] if collect else []
+    runner = _runner_for(model, method, prompt_len, prompt_len, term1_mass_exp)
+    step = _GreedyStep(model, runner, cache, first.view(1), prompt_len, n_new,
+                       mask=torch.cat([attention_mask, torch.ones_like(first)], dim=1))
+    n_done = 1
+    with condition_block_decode_context(runner), torch.no_grad():
+        while n_done < n_new and not bool(torch.isin(step.tokens[n_done - 1], stop_ids)):
+            runner.reset_step(prompt_len + n_done - 1)
+            step()
+            if collect:
+                metadata.append(runner.summarize())
+            n_done += 1
+            step.mask = torch.cat([step.mask, step.mask.new_ones((1, 1))], dim=1)
+    return step.tokens[:n_done].view(1, -1).to(input_ids.dtype), summarize_condition_block_step_metadata(metadata)
 
 
 def _generate_condition_block_cuda_graph(*, model, tokenizer, input_ids, attention_mask, method, dataset=None,
                                          term1_mass_exp=False):
     """One graph replay per generated token (CBT/core.py:189-314): SDPA prefill, the
-    prompt KV moved into a StaticCache, three eager warm-up steps (summaries and
-    workspaces), then the whole decode step (forward, argmax, state advance) captured
-    once and replayed.  Requires CONDITION_BLOCK_SKIP_STATS=1 and
-    full_attention_layers=0; stop tokens are applied by truncation afterwards."""
-    if os.environ.get("CONDITION_BLOCK_SKIP_STATS") != "1":
+    prompt K/V moved into a ``StaticCache``, a few eager steps on a side stream
+    (summaries and workspaces are allocated there), then the decode step captured
+    once and replayed; stop tokens truncate the output afterwards.  Requires
+    ``CONDITION_BLOCK_SKIP_STATS=1``, ``full_attention_layers=0`` and a block size
+    that is a positive multiple of 16 (every such size runs the fused HIP path)."""
+    if not _env_on(_SKIP_STATS):
         raise ValueError("CONDITION_BLOCK_CUDA_GRAPH=1 requires CONDITION_BLOCK_SKIP_STATS=1.")
     if int(method.full_attention_layers) != 0:
         raise ValueError("CUDA-graph decode supports full_attention_layers=0 only.")
-    if int(method.condition_block_size) <= 0 or int(method.condition_block_size) % 16:
+    block = int(method.condition_block_size)
+    if block <= 0 or block % 16:
         raise ValueError("CUDA-graph decode requires a block size that is a positive multiple of 16.")
-    prompt_len = int(input_ids.shape[1])
-    max_new_tokens = int(method.max_new_tokens)
-    if max_new_tokens <= 0:
-        return (torch.empty((1, 0), device=input_ids.device, dtype=input_ids.dtype),
-                summarize_condition_block_step_metadata([]))
-    with model_attention_implementation(model, "sdpa"), torch.no_grad():
-        outputs = model(input_ids=input_ids, attention_mask=attention_mask, use_cache=True, logits_to_keep=1)
-    past_key_values = _static_cache_from_prefill(model.config, outputs.past_key_values,
-                                                 max_cache_len=prompt_len + max_new_tokens)
-    dev = input_ids.device
-    out_tokens = torch.zeros(max_new_tokens, dtype=input_ids.dtype, device=dev)
-    next_id = torch.argmax(outputs.logits.float()[:, -1, :], dim=-1)
-    out_tokens[0] = next_id[0]
-    del outputs
-    input_ids_buf = next_id.view(1, 1).clone()
-    cache_pos_buf = torch.tensor([prompt_len], device=dev, dtype=torch.long)
-    step_idx_buf = torch.ones(1, device=dev, dtype=torch.long)
-    runner = ConditionBlockDecodeRunner(model=model, model_config=model.config,
-                                        layer_idx_list=list(range(int(model.config.num_hidden_layers))),
-                                        full_attention_layers=method.full_attention_layers,
-                                        block_size=method.condition_block_size, eps=method.condition_eps,
-                                        prompt_len=prompt_len, pos=prompt_len, prompt_prefix_cache={},
-                                        term1_mass_exp=term1_mass_exp)
+    prompt_len, n_new = int(input_ids.shape[1]), int(method.max_new_tokens)
+    if n_new <= 0:
+        return input_ids.new_empty((1, 0)), summarize_condition_block_step_metadata([])
+    first, cache = _prefill(model, input_ids, attention_mask)
+    cache = _static_cache_from_prefill(model.config, cache, prompt_len + n_new)
+    runner = _runner_for(model, method, prompt_len, prompt_len, term1_mass_exp)
     runner.static_suffix = True
     runner.suffix_len_dev.fill_(1)
-
-    def _decode_step():
-        step_outputs = model(input_ids=input_ids_buf, attention_mask=None, past_key_values=past_key_values,
-                             use_cache=True, logits_to_keep=1, cache_position=cache_pos_buf)
-        step_next = torch.argmax(step_outputs.logits.float()[0, -1], dim=-1)
-        out_tokens.index_copy_(0, step_idx_buf, step_next.view(1))
-        input_ids_buf.copy_(step_next.view(1, 1))
-        cache_pos_buf.add_(1)
-        step_idx_buf.add_(1)
-        runner.suffix_len_dev.add_(1)
-
-    warmup_steps = min(3, max_new_tokens - 1)
+    step = _GreedyStep(model, runner, cache, first.view(1), prompt_len, n_new, advance_suffix=True)
+    eager_steps = min(3, n_new - 1)
     with condition_block_decode_context(runner), _no_causal_mask_context(), torch.no_grad():
-        side_stream = torch.cuda.Stream()
-        side_stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side_stream):
-            for _ in range(warmup_steps):
-                _decode_step()
-        torch.cuda.current_stream().wait_stream(side_stream)
-        remaining = max_new_tokens - 1 - warmup_steps
-        if remaining > 0:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(eager_steps):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        if n_new - 1 > eager_steps:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                _decode_step()
-            for _ in range(remaining):
+                step()
+            for _ in range(n_new - 1 - eager_steps):
                 graph.replay()
     torch.cuda.synchronize()
-    tokens = out_tokens.tolist()
-    stop_token_ids = set(_stop_token_ids(tokenizer, dataset))
-    n_keep = len(tokens)
-    for idx, token in enumerate(tokens):
-        if token in stop_token_ids:
-            n_keep = idx + 1
-            break
-    output_ids = out_tokens[:n_keep].view(1, -1).to(dtype=input_ids.dtype)
-    return output_ids, {"condition_block_stats_disabled": True, "cuda_graph_decode": True}
+    stops = set(_stop_token_ids(tokenizer, dataset))
+    tokens = step.tokens.tolist()
+    n_keep = next((i + 1 for i, t in enumerate(tokens) if t in stops), len(tokens))
+    out = step.tokens[:n_keep].view(1, -1).to(input_ids.dtype)
+    return out, {"condition_block_stats_disabled": True, "cuda_graph_decode": True}

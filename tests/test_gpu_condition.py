@@ -353,3 +353,26 @@ def test_sdpa_full_attention_forward(bsz, hq, hkv, t_len, dt, device):
     for bi in range(bsz):
         exp = A.dense_decode(q[bi, :, 0], k[bi], v[bi])
         np.testing.assert_allclose(_np(out[bi, 0]), exp, atol=TOL[dt], rtol=0)
+
+
+def test_sdpa_full_attention_forward_masks(device):
+    """A prefix mask (keys [0, n) allowed) runs the HIP dense decode over those keys;
+    a left-padded mask (keys not a prefix) is detected and gives the masked attention
+    as well (transformers' SDPA), never a silently wrong prefix."""
+    announce("dense sdpa with prefix and left-padded masks")
+    rng = np.random.default_rng(77)
+    bsz, hq, hkv, t_len, d = 2, 8, 2, 300, 128
+    q = rng.standard_normal((bsz, hq, 1, d), dtype=np.float32)
+    k = rng.standard_normal((bsz, hkv, t_len, d), dtype=np.float32)
+    v = rng.standard_normal((bsz, hkv, t_len, d), dtype=np.float32)
+    tq, tk, tv = (torch.from_numpy(x).to(device) for x in (q, k, v))
+    for name, allowed in (("prefix", np.arange(t_len)[None, :] < np.array([[250], [300]])),
+                          ("left-pad", np.arange(t_len)[None, :] >= np.array([[40], [0]]))):
+        mask = torch.zeros((bsz, 1, 1, t_len), dtype=torch.float32)
+        mask[torch.from_numpy(~allowed)[:, None, None, :]] = torch.finfo(torch.float32).min
+        out, _ = cb._sdpa_full_attention_forward(None, tq, tk, tv, mask.to(device), d ** -0.5)
+        torch.cuda.synchronize()
+        for bi in range(bsz):
+            keep = allowed[bi]
+            exp = A.dense_decode(q[bi, :, 0], k[bi][:, keep], v[bi][:, keep])
+            np.testing.assert_allclose(_np(out[bi, 0]), exp, atol=1e-4, rtol=0, err_msg=name)

@@ -138,6 +138,30 @@ def test_graph_loop_matches_eager_loop(device, monkeypatch):
     assert torch.equal(eager, graphed), (eager, graphed)
 
 
+@pytest.mark.parametrize("graph", [False, True])
+def test_static_cache_loops_match_dense_tokens(device, monkeypatch, graph):
+    """eps = 0 (every block selected: exact attention) through the static-cache loops:
+    the prompt K/V moved into a StaticCache and the decode steps written after it, so
+    the greedy tokens equal the dense model's."""
+    from interattn_amd.decode import generate_condition_block_cached
+
+    announce(f"static-cache decode loop, graph={graph}, eps=0 vs dense")
+    model = _model(device)
+    ids = torch.randint(0, 256, (1, 190), generator=torch.Generator().manual_seed(5)).to(device)
+    ref_tok, _ = _dense_greedy(model, ids, 9)
+    monkeypatch.setenv("CONDITION_BLOCK_SKIP_STATS", "1")
+    if graph:
+        monkeypatch.setenv("CONDITION_BLOCK_CUDA_GRAPH", "1")
+        monkeypatch.delenv("CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE", raising=False)
+    else:
+        monkeypatch.delenv("CONDITION_BLOCK_CUDA_GRAPH", raising=False)
+        monkeypatch.setenv("CONDITION_BLOCK_POST_PREFILL_STATIC_CACHE", "1")
+    out, _ = generate_condition_block_cached(model=model, tokenizer=None, input_ids=ids,
+                                             attention_mask=torch.ones_like(ids), method=_method(0.0, 9),
+                                             device=device)
+    assert torch.equal(out, ref_tok), (out, ref_tok)
+
+
 def test_runner_no_blocks_selected(device):
     announce("decode runner eps=1e9")
     model = _model(device, dtype=torch.bfloat16, head_dim=128)

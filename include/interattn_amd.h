@@ -8,10 +8,12 @@
  * non-zero IA_ERR_* code.  ia_last_error() returns the message of the last
  * failure on the calling thread.  Scratch memory comes from a caller-owned
  * workspace whose size is given by the matching *_workspace_size() function,
- * 256-byte aligned; its contents need no initialisation.  Calls that share one workspace must not
- * overlap.  No kernel synchronises across workgroups inside a launch: multi-step
- * work (score -> select, split-K partials -> merge) is ordered by kernel
- * boundaries on the caller's stream.
+ * 256-byte aligned; its contents need no initialisation, except for
+ * ia_sparse_topk_decode (zero-filled once, see there).  Calls that share one
+ * workspace must not overlap.  Multi-step work (score -> select, split-K partials
+ * -> merge) is ordered by kernel boundaries on the caller's stream, except inside
+ * ia_sparse_topk_decode, whose one launch hands data between workgroups through
+ * flags with bounded waits.
  *
  * Reference paths below are relative to the reference repository root;
  * CBT = llama/script/analysis/condition_block_gen/methods/condition_block_triton_impl,
@@ -146,23 +148,45 @@ IA_API int ia_append_kv(const ia_paged_kv* kv, const void* k_new, const void* v_
                         int32_t head_dim, void* stream);
 
 /*
- * Top-k block selection.  score[b,h,j] = mean_g(q[b,h*G+g] . k_bar[b,h,j]) / sqrt(D)
- * (group-mean representative score of CBG/methods/quest.py:91-103 with the mean
- * key as representative).  Per (b, h) the result is the forced blocks (the
- * first forced_first and last forced_last valid blocks) plus the top k_eff of
- * the others by score, ties to the lower index, with k_eff = k - #forced when
- * forced_in_k else k (k_per_seq, a device array [batch], overrides k per
- * sequence when non-NULL).  idx[b, h, 0:n_sel[b,h]] receives the chosen block ids in
- * ascending order (idx row stride k_cap >= k_eff + #forced).  scores may be
- * NULL; otherwise it receives [batch, Hkv, nb_max] float32 (-inf past the end).
- * k_bar: [batch, Hkv, nb_max, D] of k_bar_dtype (IA_F32 or IA_BF16) at
- * (b * kbar_batch_stride + h * kbar_head_stride + j * D).
- * New entry point: the reference selects by an eps threshold only
+ * The block keys a top-k rule scores, one row of head_dim contiguous elements per
+ * block: row j of (b, h) at b * batch_stride + h * head_stride + j * head_dim
+ * elements (16-byte aligned rows).
+ *   IA_SCORE_MEAN_KEY: score = mean_g(q[b, h*G+g] . k_bar[b, h, j]) / sqrt(D), the
+ *     group-mean representative score of CBG/methods/quest.py:101 with the block's
+ *     mean key as representative (k_bar);
+ *   IA_SCORE_QUEST: score = mean_g sum_d max(q_gd k_max_d, q_gd k_min_d), Quest's page
+ *     bound (CBG/methods/quest.py:97-101; k_max, k_min).
+ * The mean-key score has no "+ log(count)" term: every block but the last holds
+ * block_size tokens, so the term is a constant that cannot change the order, and
+ * the Quest rule the top-k configurations follow ranks pages by q.k alone.
+ */
+enum {
+  IA_SCORE_MEAN_KEY = 0,
+  IA_SCORE_QUEST = 1,
+};
+typedef struct ia_block_keys {
+  int32_t score; /* IA_SCORE_MEAN_KEY or IA_SCORE_QUEST */
+  int32_t dtype; /* IA_F32 or IA_BF16 (every key array) */
+  const void* k_bar;
+  const void* k_max;
+  const void* k_min;
+  int64_t batch_stride, head_stride;
+} ia_block_keys;
+
+/*
+ * Top-k block selection.  Per (b, h) the result is the forced blocks (the first
+ * forced_first and last forced_last valid blocks) plus the top k_eff of the others
+ * by score (ia_block_keys), ties to the lower index, with k_eff = k - #forced when
+ * forced_in_k else k (k_per_seq, a device array [batch], overrides k per sequence
+ * when non-NULL).  idx[b, h, 0:n_sel[b,h]] receives the chosen block ids in
+ * ascending order (idx row stride k_cap >= k_eff + #forced).  scores may be NULL;
+ * otherwise it receives [batch, Hkv, nb_max] float32 (-inf past the end).
+ * The selection rule is the group-mean + torch.topk of CBG/methods/quest.py:91-103;
+ * the reference's condition-block path selects by an eps threshold instead
  * (_select_prompt_blocks_triton, CBT/core.py:701-744).
  */
 IA_API size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t nb_max);
-IA_API int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_bar,
-                   int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
+IA_API int ia_select_topk(const ia_decode_shape* shape, const void* q, const ia_block_keys* keys,
                    const int32_t* seq_lens, int32_t block_size, int32_t nb_max, int32_t k,
                    const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last,
                    int32_t forced_in_k,
@@ -298,16 +322,25 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
                                 size_t workspace_bytes, void* stream);
 
 /*
- * One top-k decode-attention layer call: block scores (as ia_select_topk computes
- * them, bit for bit) by a many-workgroup scorer whose first workgroup also writes
- * the finalize's launch plan (items per (sequence, kv head) from the rule's block
- * counts), then the paged finalize whose prologue stages each (sequence, kv head)'s
- * score row in LDS and applies ia_select_topk's rule (forced blocks, k or k_per_seq,
- * ties to the lower index) before streaming its share of the chosen blocks; the
- * split-K merge follows.
- * Equal to ia_select_topk + ia_sparse_paged_decode.  idx/n_sel (optional,
+ * One top-k decode-attention layer call in one launch.  One flat grid of about one
+ * workgroup per CU; each (sequence, kv head) row is split into items in proportion
+ * to the blocks its rule selects.  Item i of a row scores its share of the row's
+ * blocks (as ia_select_topk computes them, bit for bit), the row's items exchange
+ * their score ranges, every item applies ia_select_topk's rule (forced blocks, k or
+ * k_per_seq, ties to the lower index) to the whole row and streams its share of
+ * the chosen blocks, and the last item of the row to finish merges the items'
+ * split-K partials into the output.  The items of a row hand each other their
+ * scores through the workspace as tagged entries, waiting for a partner's at most
+ * the wait limit (ia_set_wait_limit); scores still missing then are computed by
+ * the waiting item itself, so the result never depends on timing.  Equal to
+ * ia_select_topk + ia_sparse_paged_decode, bit for bit.  idx/n_sel (optional,
  * together) receive the selection.  Requires nb_max <= 4096 and k_cap <= 512
- * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  Replaces the selection +
+ * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  The workspace
+ * (ia_sparse_topk_decode_workspace_size bytes) must be zero-filled before its first
+ * use and then left to the library, and used with one set of (batch, n_kv_heads,
+ * group, head_dim, nb_max, k_cap) (zero-fill it again for another): it carries a
+ * per-row call count and finished-item count from call to call.  Calls that share
+ * a workspace must not overlap.  Replaces the selection +
  * finalize pair of one decode step, _select_prompt_blocks_triton +
  * _condition_block_decode_output_fused_triton (CBT/core.py:701-744, :1035-1155),
  * for the BASELINE's top-k rule.
@@ -315,12 +348,20 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
 IA_API size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
                                                    int32_t head_dim, int32_t nb_max, int32_t k_cap);
 IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
-                                 const int32_t* seq_lens, const void* k_bar, int32_t k_bar_dtype,
-                                 int64_t kbar_batch_stride, int64_t kbar_head_stride, int32_t block_size,
+                                 const int32_t* seq_lens, const ia_block_keys* keys, int32_t block_size,
                                  int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
                                  int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale, void* out,
                                  int32_t out_dtype, int32_t* idx, int32_t* n_sel, void* workspace,
                                  size_t workspace_bytes, void* stream);
+
+/*
+ * Bound of every wait of one workgroup on another inside ia_sparse_topk_decode, in
+ * ticks of the GPU's 100 MHz constant clock (default 2,000,000 = 20 ms; a negative
+ * value restores it).  Returns the previous bound.  Applies to calls issued after
+ * it on any thread.  A bound of 0 makes every waiting item compute the missing
+ * parts itself (the tests use it to exercise that path).  No reference counterpart.
+ */
+IA_API int64_t ia_set_wait_limit(int64_t ticks);
 
 /* Most split-K items per (b, h) the two decode entry points use for the given
  * workload (the stride of the partials); size the decode workspace with it.

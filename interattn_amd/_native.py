@@ -14,6 +14,9 @@ IA_F32 = 0
 IA_BF16 = 1
 IA_FP8_E4M3 = 2
 
+IA_SCORE_MEAN_KEY = 0
+IA_SCORE_QUEST = 1
+
 IA_OK = 0
 IA_ERR_INVALID = 1
 IA_ERR_UNSUPPORTED = 2
@@ -82,6 +85,18 @@ class BlockSummaries(ctypes.Structure):
     ]
 
 
+class BlockKeys(ctypes.Structure):
+    _fields_ = [
+        ("score", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("k_bar", ctypes.c_void_p),
+        ("k_max", ctypes.c_void_p),
+        ("k_min", ctypes.c_void_p),
+        ("batch_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+    ]
+
+
 class SuffixKV(ctypes.Structure):
     _fields_ = [
         ("k", ctypes.c_void_p),
@@ -122,13 +137,14 @@ SIGNATURES = {
     "ia_sparse_topk_decode_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "ia_sparse_topk_decode": (
         ctypes.c_int,
-        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, _P, _I32, _I64, _I64, _I32, _I32, _I32, _P,
-         _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P, _SZ, _P],
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, ctypes.POINTER(BlockKeys), _I32, _I32, _I32,
+         _P, _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P, _SZ, _P],
     ),
+    "ia_set_wait_limit": (_I64, [_I64]),
     "ia_select_topk_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "ia_select_topk": (
         ctypes.c_int,
-        [ctypes.POINTER(DecodeShape), _P, _P, _I32, _I64, _I64, _P, _I32, _I32, _I32, _P, _I32, _I32, _I32,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockKeys), _P, _I32, _I32, _I32, _P, _I32, _I32, _I32,
          _P, _I32, _P, _P, _P, _SZ, _P],
     ),
     "ia_paged_decode_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32]),

@@ -7,6 +7,16 @@
 
 namespace ia {
 
+namespace {
+constexpr int64_t kDefaultWaitTicks = 2000000;  // 20 ms of the 100 MHz clock
+std::atomic<int64_t> g_wait_ticks{kDefaultWaitTicks};
+}  // namespace
+
+int64_t wait_limit_ticks() { return g_wait_ticks.load(std::memory_order_relaxed); }
+int64_t set_wait_limit_ticks(int64_t ticks) {
+  return g_wait_ticks.exchange(ticks < 0 ? kDefaultWaitTicks : ticks, std::memory_order_relaxed);
+}
+
 int units_cap_items(int64_t units) { return (int)std::max<int64_t>(1, std::min<int64_t>(units, kMaxItemsPerBh)); }
 
 // Split-K workspace: (m, l) partials, accumulator partials, items per row.
@@ -179,41 +189,39 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   return dispatch_decode(p, kv->dtype, D, G, src, dim3(grid), st, nullptr);
 }
 
-// Plan entries a fused launch may need: its grid is at most the resident workgroups
-// (below kPlanMinEntries on any device this build targets) or n_rows x
-// ceil(s_cap / t_cap) <= n_rows x max_items when LDS bounds force small items.
-constexpr int64_t kPlanMinEntries = 4096;
-int64_t fused_plan_entries(int64_t n_rows, int k_cap) {
-  return std::max<int64_t>(kPlanMinEntries, n_rows * units_cap_items(k_cap));
-}
-
-// Fused top-k decode workspace: the score rows, the split-K partials, the plan.
-size_t fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, size_t* decode_off,
-                       size_t* plan_off) {
-  const size_t scores = align_up((size_t)batch * hkv * std::max(nb_max, 1) * 4, 256);
-  *decode_off = scores;
-  *plan_off = align_up(scores + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap)), 256);
-  return *plan_off + (size_t)fused_plan_entries((int64_t)batch * hkv, k_cap) * sizeof(PlanEntry);
+// Fused top-k decode workspace: one 256-byte line per row first (the row's
+// finished-partial count, zero between calls, and its epoch), then the published
+// score entries [row, nb_max] (8 bytes each) and the split-K partials.
+struct FusedWs {
+  size_t sbuf, decode, total;
+};
+FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap) {
+  const int64_t rows = (int64_t)batch * hkv;
+  FusedWs L;
+  L.sbuf = align_up((size_t)rows * kFlagStride * 4, 256);
+  L.decode = align_up(L.sbuf + (size_t)rows * std::max(nb_max, 1) * 8, 256);
+  L.total = align_up(L.decode + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap)), 256);
+  return L;
 }
 
 int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
-                    const void* k_bar, int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
-                    int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
-                    int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale, void* out,
-                    int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    const ia_block_keys* keys, int32_t block_size, int32_t nb_max, int32_t k,
+                    const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
+                    int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out,
+                    void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_shape(shape);
   if (rc) return rc;
   rc = check_kv(kv, shape->head_dim);
   if (rc) return rc;
-  if (!q || !out || !seq_lens || !k_bar) return fail(IA_ERR_INVALID, "q, out, seq_lens and k_bar must be non-null");
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  float score_scale = 0.f;
+  rc = check_block_keys(keys, G, D, &score_scale);
+  if (rc) return rc;
+  if (!q || !out || !seq_lens) return fail(IA_ERR_INVALID, "q, out and seq_lens must be non-null");
   if ((idx_out == nullptr) != (n_sel_out == nullptr)) return fail(IA_ERR_INVALID, "idx and n_sel go together");
   if (out_dtype != IA_F32 && out_dtype != IA_BF16) return fail(IA_ERR_INVALID, "out dtype must be IA_F32 or IA_BF16");
   if (!(scale > 0.f) || !std::isfinite(scale)) return fail(IA_ERR_INVALID, "scale must be positive and finite");
-  if (k_bar_dtype != IA_F32 && k_bar_dtype != IA_BF16) return fail(IA_ERR_INVALID, "k_bar dtype must be IA_F32 or IA_BF16");
-  const int eb = k_bar_dtype == IA_BF16 ? 2 : 4;
-  if ((kbar_batch_stride * eb) % 16 || (kbar_head_stride * eb) % 16 || reinterpret_cast<uintptr_t>(k_bar) % 16)
-    return fail(IA_ERR_INVALID, "k_bar rows must be 16-byte aligned");
   if (block_size <= 0 || block_size % 16 != 0) return fail(IA_ERR_INVALID, "block_size must be a positive multiple of 16");
   if (nb_max < 0 || k < 0 || forced_first < 0 || forced_last < 0 || k_cap <= 0)
     return fail(IA_ERR_INVALID, "nb_max, k, forced_* must be >= 0 and k_cap > 0");
@@ -221,17 +229,13 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
     return fail(IA_ERR_UNSUPPORTED, "fused top-k decode takes nb_max <= " + std::to_string(kFusedMaxBlocks) +
                                         " and k_cap <= " + std::to_string(kMaxUnitsPerItem) +
                                         "; use ia_select_topk + ia_sparse_paged_decode");
-  const int G = shape->n_q_heads / shape->n_kv_heads;
-  const int D = shape->head_dim;
-  size_t decode_off = 0, plan_off = 0;
-  const size_t need = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, &decode_off, &plan_off);
-  if (!workspace || workspace_bytes < need)
-    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
+  const FusedWs L = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(L.total) + " bytes");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   if (shape->batch == 0) return IA_OK;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = reinterpret_cast<char*>(workspace);
-  float* scores = reinterpret_cast<float*>(ws);
 
   DecodeParams p{};
   p.q = q;
@@ -242,7 +246,6 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   p.k_cap = k_cap;
   p.unit_tokens = block_size;
   p.nb_max = nb_max;
-  p.scores = scores;
   p.k_per_seq = k_per_seq;
   p.topk_k = k;
   p.forced_first = forced_first;
@@ -255,6 +258,17 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   p.q_f32 = shape->q_dtype == IA_F32;
   p.out_f32 = out_dtype == IA_F32;
   p.out = out;
+  const bool quest = keys->score == IA_SCORE_QUEST;
+  p.kb = quest ? keys->k_max : keys->k_bar;
+  p.kb2 = quest ? keys->k_min : keys->k_bar;
+  p.kb_batch_stride = keys->batch_stride;
+  p.kb_head_stride = keys->head_stride;
+  p.kb_bf16 = keys->dtype == IA_BF16;
+  p.score_quest = quest;
+  p.score_scale = score_scale;
+  p.rowctr = reinterpret_cast<u32*>(ws);
+  p.sbuf = reinterpret_cast<unsigned long long*>(ws + L.sbuf);
+  p.wait_ticks = wait_limit_ticks();
   const int cap_items = units_cap_items(k_cap);
   const int64_t bh = (int64_t)shape->batch * shape->n_kv_heads;
   p.max_items = cap_items;
@@ -262,17 +276,8 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   rc = balanced_grid(p, kv->dtype, D, G, kSrcTopkFused, bh, k_cap, block_size / 16, cap_items, st, &grid,
                      &p.plan_budget);
   if (rc) return rc;
-  if (grid > fused_plan_entries(bh, k_cap)) return fail(IA_ERR_UNSUPPORTED, "plan entries exceed the workspace");
   p.n_rows = (int)bh;
-  set_decode_ws(p, ws + decode_off, bh, cap_items, G, D);
-  PlanEntry* entries = reinterpret_cast<PlanEntry*>(ws + plan_off);
-  p.plan = entries;
-  // the scorer launch also writes the finalize's plan
-  const TopkPlanArgs plan{k, k_per_seq, forced_first, forced_last, forced_in_k, k_cap,
-                          entries, grid, p.plan_budget, cap_items, (int)bh};
-  rc = run_topk_scores(shape, q, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride, seq_lens, block_size,
-                       nb_max, scores, plan, st);
-  if (rc) return rc;
+  set_decode_ws(p, ws + L.decode, bh, cap_items, G, D);
   return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(grid), st, nullptr);
 }
 
@@ -283,20 +288,20 @@ extern "C" {
 
 size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
                                             int32_t nb_max, int32_t k_cap) {
-  size_t decode_off = 0, plan_off = 0;
-  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1), &decode_off, &plan_off);
+  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1)).total;
 }
 
 int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
-                          const void* k_bar, int32_t k_bar_dtype, int64_t kbar_batch_stride, int64_t kbar_head_stride,
-                          int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq,
-                          int32_t forced_first, int32_t forced_last, int32_t forced_in_k, int32_t k_cap, float scale,
-                          void* out, int32_t out_dtype, int32_t* idx, int32_t* n_sel, void* workspace,
-                          size_t workspace_bytes, void* stream) {
-  return ia::run_topk_decode(shape, q, kv, seq_lens, k_bar, k_bar_dtype, kbar_batch_stride, kbar_head_stride,
-                             block_size, nb_max, k, k_per_seq, forced_first, forced_last, forced_in_k, k_cap, scale,
-                             out, out_dtype, idx, n_sel, workspace, workspace_bytes, stream);
+                          const ia_block_keys* keys, int32_t block_size, int32_t nb_max, int32_t k,
+                          const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
+                          int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx, int32_t* n_sel,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return ia::run_topk_decode(shape, q, kv, seq_lens, keys, block_size, nb_max, k, k_per_seq, forced_first,
+                             forced_last, forced_in_k, k_cap, scale, out, out_dtype, idx, n_sel, workspace,
+                             workspace_bytes, stream);
 }
+
+int64_t ia_set_wait_limit(int64_t ticks) { return ia::set_wait_limit_ticks(ticks); }
 
 size_t ia_paged_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
                                       int32_t max_items) {

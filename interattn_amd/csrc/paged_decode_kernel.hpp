@@ -108,7 +108,7 @@ struct DecodeParams {
   int32_t k_cap;
   // kSrcTopkFused: block scores [batch*Hkv, nb_max] and the selection rule; item 0
   // of each (b, h) also writes the chosen ids / counts when idx_out is set
-  const float* scores;
+  float* scores;
   const int32_t* k_per_seq;
   int32_t topk_k, forced_first, forced_last, forced_in_k;
   int32_t* idx_out;
@@ -143,7 +143,19 @@ struct DecodeParams {
   int32_t* part_n;  // [batch*Hkv]
   int32_t plan_budget;
   int32_t n_rows;
-  const PlanEntry* plan;
+  // fused top-k call: block keys scored in the prologue (k_bar for the mean-key
+  // score, or k_max / k_min for the Quest score), rows of D contiguous elements at
+  // b * kb_batch_stride + h * kb_head_stride + j * D; hand-off flags between the
+  // items of a row (zero between calls) and the bound of every wait on them
+  const void* kb;
+  const void* kb2;
+  int64_t kb_batch_stride, kb_head_stride;
+  int32_t kb_bf16;
+  int32_t score_quest;
+  float score_scale;
+  unsigned long long* sbuf;  // [rows, nb_max] published scores: tag << 32 | score bits
+  u32* rowctr;               // [rows, kFlagStride]: finished partials (word 0), row epoch (word 1)
+  int64_t wait_ticks;
 };
 
 constexpr int kWaves = 4;  // split-K merge
@@ -278,6 +290,212 @@ __device__ __forceinline__ int plan_row_units(const DecodeParams& p, int r) {
   }
 }
 
+
+// ------------------------------------------------------------ fused top-k call helpers
+
+// Block scores of one (sequence, kv head), blocks [lo, hi), by the whole workgroup:
+// in step t wave w scores block base + 32 t + 4 w + r (lane row r; 16 lanes per key
+// row), NB steps in flight.  Mean key: s = sum_g q_g . k_bar / (G sqrt(D)); Quest:
+// s = sum_g sum_d max(q_gd k_max_d, q_gd k_min_d) / G = (q+ . k_max + q- . k_min) / G
+// with q+ = sum_g max(q_g, 0), q- = sum_g min(q_g, 0) (qa, qb).  The arithmetic is
+// the standalone selector's (block_score / block_score_quest), so both give the same
+// bits.  Scores land in s_lds[j].
+template <int D, bool KBF16, bool QUEST>
+__device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_off, int lo, int hi, const float* qa,
+                                             const float* qb, float* s_lds) {
+  constexpr int DPL = D / 16;
+  constexpr int EB = KBF16 ? 2 : 4;
+  constexpr int NWR = DPL * EB / 4;                  // words per lane per key row
+  constexpr int NW = D >= 128 ? 64 : 32;             // key words per lane in flight
+  constexpr int NS = NW / NWR / (QUEST ? 2 : 1);     // steps in flight (Quest reads two rows per block)
+  typedef u32 __attribute__((ext_vector_type(NW))) words_t;  // a value: registers, never memory
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c16 = lane & 15;
+  const int r = lane >> 4;
+  const char* k1 = reinterpret_cast<const char*>(p.kb) + kb_off * EB;
+  const char* k2 = reinterpret_cast<const char*>(p.kb2) + kb_off * EB;
+  for (int base = lo; base < hi; base += 32 * NS) {
+    words_t w;
+    // the loads of every step that holds a block of the range are issued without a
+    // per-lane condition (rows past hi re-read row hi - 1); steps past it are skipped
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (base + 32 * t >= hi) break;  // uniform
+      const int j = min(base + 32 * t + 4 * wave + r, hi - 1);
+#pragma unroll
+      for (int q = 0; q < (QUEST ? 2 : 1); ++q) {
+        const char* rowp = (q ? k2 : k1) + ((int64_t)j * D + c16 * DPL) * EB;
+        const int o = (QUEST ? 2 * t + q : t) * NWR;
+        if constexpr (NWR >= 4) {
+#pragma unroll
+          for (int v4 = 0; v4 < NWR; v4 += 4) {
+            const u32x4_t x = ld_stream16(rowp + 4 * v4);
+            w[o + v4] = x[0];
+            w[o + v4 + 1] = x[1];
+            w[o + v4 + 2] = x[2];
+            w[o + v4 + 3] = x[3];
+          }
+        } else {
+          const u32x2_t x = ld_stream8(rowp);
+          w[o] = x[0];
+          w[o + 1] = x[1];
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NS; ++t) {
+      if (base + 32 * t >= hi) break;  // uniform
+      const int j = base + 32 * t + 4 * wave + r;
+      u32 w1[NWR], w2[NWR];
+#pragma unroll
+      for (int e = 0; e < NWR; ++e) {
+        w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
+        w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
+      }
+      const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qa, qb, p.score_scale)
+                            : block_score<DPL, KBF16>(w1, qa, p.score_scale);
+      if (c16 == 0 && j < hi) s_lds[j] = a;
+    }
+  }
+}
+
+constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
+constexpr int kMergeFastSlots = 8;  // slots per wave read in the merge's one-round-trip path
+constexpr int kMergeGroup = kMergeFastSlots;            // slots per merge group
+constexpr int kMergeGroups = kMaxItemsPerBh / kMergeGroup;  // groups of a row's split-K items
+constexpr int kFlagStride = 64;  // u32 words between hand-off flags (one 256-byte line each)
+
+// The split-K merge of a row's items (balanced launches: the merge kernel and the
+// fused top-k call's in-kernel merge share it, so both give the same bits).  Slots
+// are taken in groups of kMergeGroup: a group's partial is M = max_j m_j,
+// L = sum_j f_j l_j, a = sum_j f_j acc_j with f_j = 2^(m_j - M), slots in order
+// (absent slots hold m = -inf); the groups are combined the same way, in order, and
+// out = a / max(L, 1e-30) (CBT/legacy.py:765-794).  One lane holds PER consecutive
+// outputs of the row's [G, D] block, all of one query row.
+template <int PER>
+__device__ __forceinline__ void merge_group(const float* mv, const float* lv, const float (*av)[PER], float& M,
+                                            float& L, float* a) {
+  M = kNegInf;
+#pragma unroll
+  for (int j = 0; j < kMergeGroup; ++j) M = fmaxf(M, mv[j]);
+  L = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) a[e] = 0.f;
+  if (M != kNegInf) {
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j) {
+      const float f = (mv[j] == kNegInf) ? 0.f : exp2f(mv[j] - M);
+      L += f * lv[j];
+#pragma unroll
+      for (int e = 0; e < PER; ++e) a[e] = fmaf(f, av[j][e], a[e]);
+    }
+  }
+}
+
+// Combine ng <= kMergeGroups group partials in order (gm/gl/ga give group g's M, L
+// and outputs; the loop bound is a constant so that register arrays stay in
+// registers); writes the PER outputs of the lane through store(e, value).
+template <int PER, typename GM, typename GL, typename GA, typename Store>
+__device__ __forceinline__ void merge_combine(int ng, GM gm, GL gl, GA ga, Store store) {
+  float M = kNegInf;
+#pragma unroll
+  for (int g = 0; g < kMergeGroups; ++g)
+    if (g < ng) M = fmaxf(M, gm(g));
+  float L = 0.f, a[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) a[e] = 0.f;
+  if (M != kNegInf) {
+#pragma unroll
+    for (int g = 0; g < kMergeGroups; ++g) {
+      if (g < ng) {
+        const float mg = gm(g);
+        const float f = (mg == kNegInf) ? 0.f : exp2f(mg - M);
+        L += f * gl(g);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) a[e] = fmaf(f, ga(g, e), a[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) store(e, a[e] / fmaxf(L, 1e-30f));
+}
+
+// The fused call's in-kernel split-K merge, run by the row's last item to finish
+// (every thread of its workgroup calls it): the row's n partials are read at the
+// coherence point and merged with the merge kernel's merge_group / merge_combine
+// arithmetic, so the output equals the two-step path's bit for bit (which lane
+// computes an output does not change its arithmetic).  Each thread merges outputs
+// o = threadIdx.x + kFinThreads k; the first pass's slot loads are issued together
+// with the (m, l) loads that are staged in LDS, so the merge costs one round trip.
+template <int D, int G>
+__device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h, int bh, int n) {
+  constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
+  __shared__ float ml_lds[kMaxItemsPerBh][G][2];
+  const int64_t slot0 = (int64_t)bh * p.max_items;
+  float acc[kMergeGroups][kMergeGroup];
+  auto load_acc = [&](int o) {
+#pragma unroll
+    for (int g = 0; g < kMergeGroups; ++g) {
+#pragma unroll
+      for (int j = 0; j < kMergeGroup; ++j) {
+        const int s = kMergeGroup * g + j;
+        acc[g][j] = s < n ? ld_agent(p.part_acc + (slot0 + s) * (G * D) + o) : 0.f;
+      }
+    }
+  };
+  if (threadIdx.x < G * D) load_acc(threadIdx.x);
+  constexpr int kMlPer = (kMaxItemsPerBh * G + kFinThreads - 1) / kFinThreads;
+  float mlv[kMlPer][2];
+#pragma unroll
+  for (int i = 0; i < kMlPer; ++i) {
+    const int t = threadIdx.x + kFinThreads * i;
+    if (t < n * G) {
+      mlv[i][0] = ld_agent(p.part_ml + (slot0 * G + t) * 2);
+      mlv[i][1] = ld_agent(p.part_ml + (slot0 * G + t) * 2 + 1);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kMlPer; ++i) {
+    const int t = threadIdx.x + kFinThreads * i;
+    if (t < n * G) {
+      ml_lds[t / G][t % G][0] = mlv[i][0];
+      ml_lds[t / G][t % G][1] = mlv[i][1];
+    }
+  }
+  const int ng = (n + kMergeGroup - 1) / kMergeGroup;
+  __syncthreads();
+  // one output per pass (G * D > kFinThreads takes several passes)
+#pragma unroll 1
+  for (int k = 0; k < NO; ++k) {
+    const int o = threadIdx.x + kFinThreads * k;
+    if (o >= G * D) break;
+    if (k > 0) load_acc(o);
+    const int g0 = o / D;
+    float gM[kMergeGroups], gL[kMergeGroups], ga[kMergeGroups][1];
+#pragma unroll
+    for (int g = 0; g < kMergeGroups; ++g) {
+      gM[g] = kNegInf;
+      gL[g] = 0.f;
+      ga[g][0] = 0.f;
+      if (g < ng) {
+        float mv[kMergeGroup], lv[kMergeGroup], av[kMergeGroup][1];
+#pragma unroll
+        for (int j = 0; j < kMergeGroup; ++j) {
+          const int s = kMergeGroup * g + j;
+          mv[j] = s < n ? ml_lds[s][g0][0] : kNegInf;
+          lv[j] = s < n ? ml_lds[s][g0][1] : 0.f;
+          av[j][0] = acc[g][j];
+        }
+        merge_group<1>(mv, lv, av, gM[g], gL[g], ga[g]);
+      }
+    }
+    merge_combine<1>(
+        ng, [&](int g) { return gM[g]; }, [&](int g) { return gL[g]; }, [&](int g, int) { return ga[g][0]; },
+        [&](int, float v) { store_decode_out<G, D>(p, b, h, o, v); });
+  }
+}
+
 template <int D, int G, typename KV, int SRC>
 __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
@@ -311,6 +529,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ float wl_lds[kFinWaves][G];
 
   __shared__ PlanEntry plan_lds;
+  __shared__ u32 merge_todo[1];  // fused top-k call: this workgroup merges its row
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -351,30 +570,21 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     }
   };
-  // fused top-k: the row's score row (-inf past its sequence, up to nb_max)
-  constexpr int kScPer = SRC == kSrcTopkFused ? kFusedMaxBlocks / kFinThreads : 1;
-  float scv[kScPer];
-  auto load_scores = [&](int row) {
-    const float* sr = p.scores + (int64_t)row * p.nb_max;
-#pragma unroll
-    for (int i = 0; i < kScPer; ++i) {
-      const int t = threadIdx.x + i * kFinThreads;
-      scv[i] = t < p.nb_max ? sr[t] : kNegInf;
-    }
-  };
-
-  int spec_row = -1;
+  u32 row_epoch = 0u;  // fused top-k call: calls so far that split this row
   if constexpr (kBalanced) {
     PlanEntry e;
     if constexpr (SRC == kSrcTopkFused) {
-      // the plan entry, the query rows and the score row in one round trip: the
-      // last two for the row of an even split (the plan's row whenever every row has
-      // the same work), fetched again after the entry on a miss
-      spec_row = (int)(((long long)blockIdx.x * p.n_rows) / gridDim.x);
-      const int sb = spec_row / p.n_kv_heads;
-      load_q(sb, spec_row - sb * p.n_kv_heads);
-      load_scores(spec_row);
-      e = p.plan[blockIdx.x];
+      // every wave evaluates the launch plan itself (no barrier, no round trip to a
+      // plan written elsewhere): a row's units are the blocks the top-k rule takes
+      auto slots_of = [&](int rr) -> int {
+        const int bb = rr / p.n_kv_heads;
+        const int kr = p.k_per_seq ? max(p.k_per_seq[bb], 0) : p.topk_k;
+        const int nbs_r = min(cdiv_pos(max(p.seq_lens[bb], 0), p.unit_tokens), p.nb_max);
+        return topk_count(nbs_r, TopkRule{p.forced_first, p.forced_last, kr, p.forced_in_k, p.k_cap}) * nsub_u;
+      };
+      PlanRows rows;
+      const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
+      e = plan_entry_wave(slots_of, rows, p.n_rows, rule, (int)blockIdx.x, nsub_u);
     } else {
       if (wave == 0) {
         PlanRows rows;
@@ -395,40 +605,114 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     slot_lo = __builtin_amdgcn_readfirstlane(e.slot_lo);
     slot_hi = __builtin_amdgcn_readfirstlane(e.slot_hi);
     n_units = __builtin_amdgcn_readfirstlane(e.n_units);
-    if constexpr (SRC == kSrcTopkFused) {
-      seq_len = __builtin_amdgcn_readfirstlane(e.seq_len);
-      k_b = __builtin_amdgcn_readfirstlane(e.k_row);
-      if (row != spec_row) load_scores(row);
-    } else {
-      seq_len = max(p.seq_lens[b], 0);
-    }
+    seq_len = max(p.seq_lens[b], 0);
+    if constexpr (SRC == kSrcTopkFused) k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
   } else {
     b = blockIdx.z;
     h = blockIdx.y;
     item = blockIdx.x;
   }
   const int bh = b * p.n_kv_heads + h;
-  if (bh != spec_row) load_q(b, h);
+  if constexpr (SRC == kSrcTopkFused)
+    if (n_items_row > 1) row_epoch = __builtin_amdgcn_readfirstlane(ld_agent_u32(p.rowctr + (int64_t)bh * kFlagStride + 1));
+  load_q(b, h);
 
   if constexpr (SRC == kSrcTopkFused) {
-    // the whole score row in LDS, then the shared top-k rule (every item of the row
-    // selects the same blocks; item 0 publishes them)
+    // ---- block scores: item i of the row's n scores blocks [i nbs / n, (i+1) nbs / n)
+    // into LDS and publishes them as tagged 8-byte entries, score bits | tag << 32 with
+    // tag = the row's epoch + 1 (the epoch counts the calls that split the row, so an
+    // entry left by an earlier call never matches).  Each item takes the other items'
+    // blocks from the entries whose tag has arrived; when one is still missing at the
+    // wait bound, it scores the other items' blocks itself (same arithmetic, same
+    // bits).  Every item then holds the whole row and applies the shared top-k rule
+    // (item 0 publishes the chosen blocks).
     const int nbs = min(cdiv_pos(seq_len, p.unit_tokens), p.nb_max);
+    const int n_it = n_items_row;
+    auto range_lo = [&](int i) { return (int)(((long long)i * nbs) / n_it); };
+    unsigned long long* row_entries = p.sbuf + (int64_t)bh * p.nb_max;
+    const int own_lo = range_lo(item), own_hi = range_lo(item + 1);
+    {
+      constexpr int SDPL = D / 16;  // key dims per lane (16 lanes per key row)
+      float qa[SDPL], qb[SDPL];     // mean key: qa = sum_g q_g; Quest: qa = sum_g q_g+, qb = sum_g q_g-
+#pragma unroll
+      for (int e = 0; e < SDPL; ++e) {
+        qa[e] = 0.f;
+        qb[e] = 0.f;
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const int64_t qrow = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * SDPL;
+        float v[SDPL];
+        if (p.q_f32) {
+#pragma unroll
+          for (int e = 0; e < SDPL; ++e) v[e] = reinterpret_cast<const float*>(p.q)[qrow + e];
+        } else {
+          u32 w[SDPL / 2];
+          load_words<SDPL / 2>(reinterpret_cast<const char*>(reinterpret_cast<const unsigned short*>(p.q) + qrow), w);
+#pragma unroll
+          for (int e = 0; e < SDPL / 2; ++e) {
+            v[2 * e] = bf16_lo(w[e]);
+            v[2 * e + 1] = bf16_hi(w[e]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < SDPL; ++e) {
+          if (p.score_quest) {
+            qa[e] += fmaxf(v[e], 0.f);
+            qb[e] += fminf(v[e], 0.f);
+          } else {
+            qa[e] += v[e];  // same order as the standalone selector's sum
+          }
+        }
+      }
+      const int64_t kb_off = (int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride;
+      // blocks [lo, hi): 32 per workgroup step (wave w, lane row r: block 32 t + 4 w + r)
+      auto score_range = [&](int lo, int hi) {
+        if (p.score_quest) {
+          if (p.kb_bf16) score_blocks<D, true, true>(p, kb_off, lo, hi, qa, qb, fsc);
+          else score_blocks<D, false, true>(p, kb_off, lo, hi, qa, qb, fsc);
+        } else {
+          if (p.kb_bf16) score_blocks<D, true, false>(p, kb_off, lo, hi, qa, qb, fsc);
+          else score_blocks<D, false, false>(p, kb_off, lo, hi, qa, qb, fsc);
+        }
+      };
+      score_range(own_lo, own_hi);
+      if (n_it > 1) {
+        if (threadIdx.x == 0) merge_todo[0] = 0u;
+        __syncthreads();
+        const u32 tag = row_epoch + 1u;
+        for (int j = own_lo + threadIdx.x; j < own_hi; j += kFinThreads)
+          st_agent_u64(row_entries + j, ((unsigned long long)tag << 32) | __float_as_uint(fsc[j]));
+        const unsigned long long t0 = clock_100mhz();
+        bool missing = false;
+        for (int j = threadIdx.x; j < nbs; j += kFinThreads) {
+          if (j >= own_lo && j < own_hi) continue;
+          unsigned long long v = ld_agent_u64(row_entries + j);
+          while ((u32)(v >> 32) != tag && (long long)(clock_100mhz() - t0) <= p.wait_ticks) {
+            __builtin_amdgcn_s_sleep(1);
+            v = ld_agent_u64(row_entries + j);
+          }
+          if ((u32)(v >> 32) == tag) fsc[j] = __uint_as_float((u32)v);
+          else missing = true;
+        }
+        if (missing) merge_todo[0] = 1u;
+        __syncthreads();
+        if (merge_todo[0]) {  // an entry missed the bound: the other items' blocks here
+          score_range(0, own_lo);
+          score_range(own_hi, nbs);
+        }
+      }
+    }
+    __syncthreads();
+    // the whole score row in LDS: the shared top-k rule
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
-    // staging the row also gives the selection its candidates' key range
     const TopkForced forced(rule, nbs);
     u32 kmx = 0u, kmn_inv = 0u;
-#pragma unroll
-    for (int i = 0; i < kScPer; ++i) {
-      const int t = threadIdx.x + i * kFinThreads;
-      if (t < nbs) {
-        const float v = scv[i];
-        fsc[t] = v;
-        if (!forced(t)) {
-          const u32 key = order_key(v);
-          kmx = max(kmx, key);
-          kmn_inv = max(kmn_inv, ~key);
-        }
+    for (int t = threadIdx.x; t < nbs; t += kFinThreads) {
+      if (!forced(t)) {
+        const u32 key = order_key(fsc[t]);
+        kmx = max(kmx, key);
+        kmn_inv = max(kmn_inv, ~key);
       }
     }
     topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
@@ -1074,6 +1358,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __syncthreads();
 
   // ---- fold the waves: one (m, l, acc) per item, or the output when the item is alone
+  // (a fused call writes its partials through to the coherence point: the row's
+  // last item to finish merges them)
   const int64_t pbase = (int64_t)bh * p.max_items + item;
   for (int o = threadIdx.x; o < G * D; o += kFinThreads) {
     const int g = o / D;
@@ -1092,6 +1378,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
     if (!split) {
       store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
+    } else if (SRC == kSrcTopkFused) {
+      st_agent(p.part_acc + pbase * (G * D) + o, a);
+      if (o % D == 0) {
+        st_agent(p.part_ml + (pbase * G + g) * 2 + 0, M);
+        st_agent(p.part_ml + (pbase * G + g) * 2 + 1, l);
+      }
     } else {
       p.part_acc[pbase * (G * D) + o] = a;
       if (o % D == 0) {
@@ -1100,10 +1392,29 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     }
   }
+  if constexpr (SRC == kSrcTopkFused) {
+    if (split) {
+      // the row's items count their finished partials; the one that brings the count
+      // to n merges (every partial is then at the coherence point) and resets the
+      // count for the next call: nobody waits, so nothing depends on which
+      // workgroups are resident together
+      wait_memory();
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        u32* ctr = p.rowctr + (int64_t)bh * kFlagStride;
+        const u32 before = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before == (u32)(n_items_row - 1);
+        if (last) {  // every item has read the epoch: advance it for the next call
+          st_agent_u32(ctr, 0u);
+          st_agent_u32(ctr + 1, row_epoch + 1u);
+        }
+        merge_todo[0] = last ? 1u : 0u;
+      }
+      __syncthreads();
+      if (merge_todo[0]) fused_merge<D, G>(p, b, h, bh, n_items_row);
+    }
+  }
 }
-
-constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
-constexpr int kMergeFastSlots = 8;  // slots per wave read in the merge's one-round-trip path
 
 // Split-K merge, one workgroup per (sequence, kv head): out = sum_s f_s acc_s / sum_s f_s l_s
 // with f_s = 2^(m_s - M) over the finalize items' partials and the route chunks'
@@ -1161,14 +1472,59 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   for (int j = 0; j < kMergeFastSlots; ++j) clear_slot(j);
   int n_fin = n_slots;
   if (counted) {
+    // groups of kMergeGroup slots: wave w takes groups w and w + kWaves; the first
+    // n_slots slots are loaded before the row's item count arrives
     n_fin = min(max(p.part_n[bh], 0), p.max_items);
+    auto slot_ptrs = [&](int s, const float*& ml, const float*& acc) {
+      const int64_t slot = (int64_t)bh * p.max_items + s;
+      ml = p.part_ml + slot * G * 2;
+      acc = p.part_acc + slot * (G * D);
+    };
 #pragma unroll
     for (int j = 0; j < kMergeFastSlots; ++j) {
       const int s = kMergeFastSlots * wave + j;
-      const int64_t slot = (int64_t)bh * p.max_items + s;
-      if (s < n_slots) load_slot(j, p.part_ml + slot * G * 2, p.part_acc + slot * (G * D));
+      if (s < n_slots) {
+        const float *ml, *acc;
+        slot_ptrs(s, ml, acc);
+        load_slot(j, ml, acc);
+      }
     }
     if (n_fin <= 1) return;  // a row of one item: the finalize wrote its output
+    const int ng = (n_fin + kMergeGroup - 1) / kMergeGroup;
+    if (ng == 1 && wave != 0) return;
+    __shared__ float gm_lds[kMergeGroups][64];
+    __shared__ float gl_lds[kMergeGroups][64];
+    __shared__ float ga_lds[kMergeGroups][G * D];
+    float gM = kNegInf, gL = 0.f, ga[PER];
+    for (int g = wave; g < ng; g += kWaves) {
+#pragma unroll
+      for (int j = 0; j < kMergeGroup; ++j) {
+        const int s = kMergeGroup * g + j;
+        if (s >= n_fin) {
+          clear_slot(j);
+        } else if (g != wave || s >= n_slots) {
+          const float *ml, *acc;
+          slot_ptrs(s, ml, acc);
+          load_slot(j, ml, acc);
+        }
+      }
+      merge_group<PER>(mv, lv, av, gM, gL, ga);
+      if (ng > 1) {
+        gm_lds[g][lane] = gM;
+        gl_lds[g][lane] = gL;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) ga_lds[g][o0 + e] = ga[e];
+      }
+    }
+    if (ng > 1) {
+      __syncthreads();
+      if (wave != 0) return;
+    }
+    merge_combine<PER>(
+        ng, [&](int g) { return ng > 1 ? gm_lds[g][lane] : gM; }, [&](int g) { return ng > 1 ? gl_lds[g][lane] : gL; },
+        [&](int g, int e) { return ng > 1 ? ga_lds[g][o0 + e] : ga[e]; },
+        [&](int e, float v) { store_decode_out<G, D>(p, b, h, o0 + e, v); });
+    return;
   }
   const int n_all = min(n_fin + n_rep, kMaxMergeSlots);
   auto ml_of = [&](int s) -> const float* {
@@ -1329,7 +1685,9 @@ template <int D, int G, typename KV, int SRC>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kFinThreads), 0, st, p);
   int rc = check_launch("paged decode");
-  if constexpr (src_balanced(SRC)) {
+  if constexpr (SRC == kSrcTopkFused) {
+    return rc;  // item 0 of each row merges inside the launch
+  } else if constexpr (src_balanced(SRC)) {
     // a flat grid of at most n_rows workgroups gives every row a single item
     if (rc || (int)grid.x <= p.n_rows) return rc;
     const int even = ((int)grid.x + p.n_rows - 1) / p.n_rows;
@@ -1379,10 +1737,11 @@ int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, 
 int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
                  int nsub_u, int cap_items, hipStream_t st, int* items_out);
 
-// Block scores of the fused top-k decode and its finalize's launch plan (select_topk.hip).
-int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
-                    int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
-                    int32_t nb_max, float* scores, const TopkPlanArgs& plan, hipStream_t st);
+// Block-keys descriptor check and score scale (select_topk.hip); the hand-off wait
+// bound of the fused top-k call (paged_decode.hip).
+int check_block_keys(const ia_block_keys* keys, int G, int D, float* score_scale);
+int64_t wait_limit_ticks();
+int64_t set_wait_limit_ticks(int64_t ticks);
 
 // Dispatch by kv dtype for one (D, G): defined in paged_decode_{bf16,f32,fp8}.hip.
 int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);

@@ -16,9 +16,9 @@
 // over the grid and the workgroups past the last item are idle.  t_hi keeps an
 // item's unit ranges and subtile list within the finalize's LDS arrays.  Every
 // function here runs in one wave, without barriers: the fused top-k launch computes
-// the plan once, in a workgroup of the scorer launch, and each finalize workgroup
-// reads its entry; the other launches compute it in one wave of each finalize
-// workgroup.  Both evaluate the same code on the same S_r, so they agree bit for bit.
+// the plan in every wave of every workgroup, the other launches in one wave of each
+// finalize workgroup.  All evaluate the same code on the same S_r, so they agree
+// bit for bit.
 #pragma once
 
 #include "topk_select.hpp"
@@ -38,16 +38,6 @@ struct PlanEntry {
   int n_units;  // units of the row
   int seq_len;  // the row's sequence length
   int k_row;    // the row's top-k k (fused source)
-};
-
-// What the scorer launch of a fused top-k decode needs to write the finalize's plan:
-// the top-k rule, where the entries go and the finalize launch's shape.
-struct TopkPlanArgs {
-  int32_t k;
-  const int32_t* k_per_seq;
-  int32_t forced_first, forced_last, forced_in_k, k_cap;
-  PlanEntry* entries;
-  int32_t grid, budget, max_items, n_rows;
 };
 
 __host__ __device__ constexpr int plan_t_cap(int nsub_u) {
@@ -87,7 +77,7 @@ struct PlanRule {
 // The plan's rule, computed by one wave (every lane returns it).  slots_of(r) gives
 // S_r for any row (rows past the register stage are read through it again).
 template <typename SlotsOf>
-__device__ PlanRule plan_rule_wave(SlotsOf slots_of, int nrows, int budget, int max_items, int nsub_u,
+__device__ __forceinline__ PlanRule plan_rule_wave(SlotsOf slots_of, int nrows, int budget, int max_items, int nsub_u,
                                    PlanRows& rows) {
   const int lane = threadIdx.x & 63;
   int ssum = 0, smax = 0;
@@ -141,7 +131,7 @@ __device__ PlanRule plan_rule_wave(SlotsOf slots_of, int nrows, int budget, int 
 // nrows) and ends the walk by returning true (a uniform value); returns the number of
 // workgroups the visited rows' items take.
 template <typename SlotsOf, typename Visit>
-__device__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, Visit visit) {
+__device__ __forceinline__ int plan_walk_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, Visit visit) {
   const int lane = threadIdx.x & 63;
   const float rt = __builtin_amdgcn_rcpf((float)max(rule.t, 1));
   int base = 0;
@@ -189,7 +179,7 @@ __device__ __forceinline__ void plan_fill(PlanEntry& e, const PlanSplit& sp, int
 // The entry of workgroup w (one wave; every lane returns it; row -1 when idle).
 // seq_len and k_row are left to the caller.
 template <typename SlotsOf>
-__device__ PlanEntry plan_entry_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, int w,
+__device__ __forceinline__ PlanEntry plan_entry_wave(SlotsOf slots_of, const PlanRows& rows, int nrows, const PlanRule& rule, int w,
                                      int nsub_u) {
   PlanEntry e{};
   e.row = -1;

@@ -32,8 +32,10 @@ constexpr int kMaxLdsScores = 8192;
 struct SelectParams {
   const void* q;
   int64_t q_batch_stride, q_row_stride;
-  const void* k_bar;
+  const void* k_bar;  // mean-key score: k_bar; Quest score: k_max
+  const void* k_min;  // Quest score
   int64_t kb_batch_stride, kb_head_stride;
+  int32_t quest;
   const int32_t* seq_lens;
   int32_t block_size, nb_max, k, forced_first, forced_last, forced_in_k;
   const int32_t* k_per_seq;  // optional [batch]
@@ -42,15 +44,11 @@ struct SelectParams {
   int32_t* n_sel;
   float* scores;  // [batch*Hkv, nb_max] or null
   int32_t n_kv_heads;
-  float score_scale;   // 1 / (G * sqrt(D))
+  float score_scale;   // 1 / (G * sqrt(D)) (mean key) or 1 / G (Quest)
   int32_t lds_scores;  // score rows of up to this many blocks stay in LDS
-  // fused top-k decode: the finalize launch's plan, written by workgroup x = 0 of the
-  // scorer launch (one entry per finalize workgroup)
-  PlanEntry* plan;
-  int32_t plan_grid, plan_budget, plan_max_items, n_rows;
 };
 
-template <int D, int G, bool QF32, bool KBF16>
+template <int D, int G, bool QF32, bool KBF16, bool QUEST>
 __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(SelectParams p) {
   constexpr int DPL = D / 16;
   extern __shared__ float sc_lds[];  // p.lds_scores floats
@@ -79,51 +77,79 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
       else qv[g][e] = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
     }
   }
-  float qm[DPL];
+  float qm[DPL], qn[DPL];  // mean key: qm = sum_g q_g; Quest: qm = sum_g q_g+, qn = sum_g q_g-
   bool have_qm = false;
 
-  // ---- scores: in step t, wave w handles row base + 64 t + 4 w + r; NR steps in flight
-  const char* kb = reinterpret_cast<const char*>(p.k_bar) +
-                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * (KBF16 ? 2 : 4);
+  // ---- scores: in step t, wave w handles row base + 64 t + 4 w + r; NS steps in
+  // flight, their key words held in one vector value (registers, never memory); the
+  // Quest score reads two key rows per block
   constexpr int EB = KBF16 ? 2 : 4;
-  constexpr int NWR = DPL * EB / 4;  // words per lane per row
-  constexpr int NR = KBF16 ? 16 : 8;
+  const char* kb = reinterpret_cast<const char*>(p.k_bar) +
+                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * EB;
+  const char* kn = reinterpret_cast<const char*>(QUEST ? p.k_min : p.k_bar) +
+                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * EB;
+  constexpr int NWR = DPL * EB / 4;                // words per lane per row
+  constexpr int NW = D >= 128 && G * DPL < 64 ? 64 : 32;  // key words per lane in flight
+  constexpr int NS = NW / NWR / (QUEST ? 2 : 1);   // steps in flight
   constexpr int kRowsPerStep = 4 * kSelWaves;
-  for (int base = 0; base < nb; base += NR * kRowsPerStep) {
-    u32 w[NR][NWR];
+  typedef u32 __attribute__((ext_vector_type(NW))) words_t;
+  for (int base = 0; base < nb; base += NS * kRowsPerStep) {
+    words_t w;
+    // loads without a per-lane condition (rows past nb re-read row nb - 1); steps
+    // wholly past nb are skipped
 #pragma unroll
-    for (int t = 0; t < NR; ++t) {
-      const int j = base + kRowsPerStep * t + 4 * wave + r;
-      if (j < nb) {
-        const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * EB;
+    for (int t = 0; t < NS; ++t) {
+      if (base + kRowsPerStep * t >= nb) break;  // uniform
+      const int j = min(base + kRowsPerStep * t + 4 * wave + r, nb - 1);
+#pragma unroll
+      for (int q = 0; q < (QUEST ? 2 : 1); ++q) {
+        const char* rowp = (q ? kn : kb) + ((int64_t)j * D + c16 * DPL) * EB;
+        const int o = (QUEST ? 2 * t + q : t) * NWR;
         if constexpr (NWR >= 4) {
 #pragma unroll
           for (int v4 = 0; v4 < NWR; v4 += 4) {
             const u32x4_t x = ld_stream16(rowp + 4 * v4);
-            w[t][v4] = x[0]; w[t][v4 + 1] = x[1]; w[t][v4 + 2] = x[2]; w[t][v4 + 3] = x[3];
+            w[o + v4] = x[0];
+            w[o + v4 + 1] = x[1];
+            w[o + v4 + 2] = x[2];
+            w[o + v4 + 3] = x[3];
           }
         } else {
           const u32x2_t x = ld_stream8(rowp);
-          w[t][0] = x[0]; w[t][1] = x[1];
+          w[o] = x[0];
+          w[o + 1] = x[1];
         }
-      } else {
-#pragma unroll
-        for (int e = 0; e < NWR; ++e) w[t][e] = 0u;
       }
     }
     if (!have_qm) {
 #pragma unroll
       for (int e = 0; e < DPL; ++e) {
-        float a = 0.f;
+        float a = 0.f, c = 0.f;
 #pragma unroll
-        for (int g = 0; g < G; ++g) a += qv[g][e];
+        for (int g = 0; g < G; ++g) {
+          if constexpr (QUEST) {
+            a += fmaxf(qv[g][e], 0.f);
+            c += fminf(qv[g][e], 0.f);
+          } else {
+            a += qv[g][e];
+          }
+        }
         qm[e] = a;
+        qn[e] = c;
       }
       have_qm = true;
     }
 #pragma unroll
-    for (int t = 0; t < NR; ++t) {
-      const float a = block_score<DPL, KBF16>(w[t], qm, p.score_scale);
+    for (int t = 0; t < NS; ++t) {
+      if (base + kRowsPerStep * t >= nb) break;  // uniform
+      u32 w1[NWR], w2[NWR];
+#pragma unroll
+      for (int e = 0; e < NWR; ++e) {
+        w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
+        w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
+      }
+      const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qm, qn, p.score_scale)
+                            : block_score<DPL, KBF16>(w1, qm, p.score_scale);
       const int j = base + kRowsPerStep * t + 4 * wave + r;
       if (c16 == 0 && j < nb) {
         if (in_lds) sc_lds[j] = a;
@@ -146,154 +172,6 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
   if (threadIdx.x == 0) p.n_sel[bh] = n;
 }
 
-// Scores of every block for the fused top-k decode (the selection itself runs in
-// the finalize's prologue): grid (1 + ceil(nb_max / kScoreBlocksPerWg), Hkv, batch),
-// 256 threads; workgroup (0, 0, 0) writes the finalize's launch plan, the others of
-// slice x = 0 exit; in slice x = 1 + bx, wave w scores blocks
-// kScoreBlocksPerWg*bx + 4*(kScoreRows*w + t) + r, t < kScoreRows, every row of a lane
-// in flight at once.  Same arithmetic as the selector's scoring (bit-identical
-// scores); -inf past the sequence's end.
-constexpr int kScoreRows = 4;                         // k_bar rows per lane
-constexpr int kScoreBlocksPerWg = 4 * 4 * kScoreRows;  // 4 waves x 4 rows per load x kScoreRows
-
-// The fused finalize's launch plan (plan.hpp), by one wave: the rows' units are the
-// counts of the top-k rule (the finalize selects exactly that many blocks).
-__device__ void write_fused_plan(const SelectParams& p) {
-  const int lane = threadIdx.x & 63;
-  const int nsub_u = p.block_size / 16;
-  auto units_of = [&](int r, int& len, int& k_row) -> int {
-    const int b = r / p.n_kv_heads;
-    len = max(p.seq_lens[b], 0);
-    k_row = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.k;
-    const int nbs = min(cdiv_pos(len, p.block_size), p.nb_max);
-    return topk_count(nbs, TopkRule{p.forced_first, p.forced_last, k_row, p.forced_in_k, p.k_cap});
-  };
-  auto slots_of = [&](int r) -> int {
-    int len, k_row;
-    return units_of(r, len, k_row) * nsub_u;
-  };
-  PlanRows rows;
-  const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.plan_max_items, nsub_u, rows);
-  if (rule.n_all > 0) {
-    // every row alike: lane-strided over the grid's workgroups, row w / n_all
-    const int s = __builtin_amdgcn_readfirstlane(rows.s[0]);  // row 0 (lane 0): every row's S
-    const int n = rule.n_all;
-    const int used = p.n_rows * n;
-    for (int w = lane; w < p.plan_grid; w += 64) {
-      PlanEntry e{};
-      e.row = -1;
-      if (w < used) {
-        const int r = w / n;
-        int len, k_row;
-        units_of(r, len, k_row);
-        plan_fill(e, plan_split(r, s, n, nsub_u), w - r * n);
-        e.seq_len = len;
-        e.k_row = k_row;
-      }
-      p.plan[w] = e;
-    }
-    return;
-  }
-  const int used = plan_walk_wave(slots_of, rows, p.n_rows, rule, [&](bool active, int r, int s, int n, int first) {
-    if (active) {
-      int len, k_row;
-      units_of(r, len, k_row);
-      const PlanSplit sp = plan_split(r, s, n, nsub_u);
-      for (int i = 0; i < n; ++i) {
-        PlanEntry e;
-        plan_fill(e, sp, i);
-        e.seq_len = len;
-        e.k_row = k_row;
-        p.plan[first + i] = e;
-      }
-    }
-    return false;
-  });
-  for (int w = used + lane; w < p.plan_grid; w += 64) {
-    PlanEntry e{};
-    e.row = -1;
-    p.plan[w] = e;
-  }
-}
-
-template <int D, int G, bool QF32, bool KBF16>
-__global__ __launch_bounds__(256) void ia_condition_block_topk_scores(SelectParams p) {
-  if (blockIdx.x == 0) {  // the plan slice: one wave of one workgroup
-    if (blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x < 64) write_fused_plan(p);
-    return;
-  }
-  const int bx = blockIdx.x - 1;
-  constexpr int DPL = D / 16;
-  constexpr int EB = KBF16 ? 2 : 4;
-  constexpr int NWR = DPL * EB / 4;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c16 = lane & 15;
-  const int r = lane >> 4;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
-  const int bh = b * p.n_kv_heads + h;
-  const int j0 = kScoreBlocksPerWg * bx + 4 * kScoreRows * wave;
-  if (j0 >= p.nb_max) return;  // whole wave
-  const int seq_len = max(p.seq_lens[b], 0);
-  const int nb = min((seq_len + p.block_size - 1) / p.block_size, p.nb_max);
-  const char* kb = reinterpret_cast<const char*>(p.k_bar) +
-                   ((int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride) * EB;
-  u32 w[kScoreRows][NWR];
-#pragma unroll
-  for (int t = 0; t < kScoreRows; ++t) {
-    const int j = j0 + 4 * t + r;
-    if (j < nb) {
-      const char* rowp = kb + ((int64_t)j * D + c16 * DPL) * EB;
-      if constexpr (NWR >= 4) {
-#pragma unroll
-        for (int v4 = 0; v4 < NWR; v4 += 4) {
-          const u32x4_t x = ld_stream16(rowp + 4 * v4);
-          w[t][v4] = x[0]; w[t][v4 + 1] = x[1]; w[t][v4 + 2] = x[2]; w[t][v4 + 3] = x[3];
-        }
-      } else {
-        const u32x2_t x = ld_stream8(rowp);
-        w[t][0] = x[0]; w[t][1] = x[1];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < NWR; ++e) w[t][e] = 0u;
-    }
-  }
-  float qm[DPL];
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) qm[e] = 0.f;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int64_t row = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL;
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      float qv;
-      if constexpr (QF32) qv = reinterpret_cast<const float*>(p.q)[row + e];
-      else qv = __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[row + e] << 16);
-      qm[e] += qv;  // same order as the selector's sum
-    }
-  }
-  float* sc_row = p.scores + (int64_t)bh * p.nb_max;
-#pragma unroll
-  for (int t = 0; t < kScoreRows; ++t) {
-    const float a = block_score<DPL, KBF16>(w[t], qm, p.score_scale);
-    const int j = j0 + 4 * t + r;
-    if (c16 == 0 && j < p.nb_max) sc_row[j] = j < nb ? a : kNegInf;
-  }
-}
-
-template <int D, int G>
-void launch_scores(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipStream_t st) {
-  if (qf32) {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, true, true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, true, false>), grid, dim3(256), 0, st, p);
-  } else {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, false, true>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_topk_scores<D, G, false, false>), grid, dim3(256), 0, st, p);
-  }
-}
-
 size_t select_ws_size(int batch, int hkv, int nb_max) {
   const size_t bh = (size_t)batch * hkv;
   return bh * (size_t)std::max(nb_max, 1) * 4;
@@ -302,56 +180,49 @@ size_t select_ws_size(int batch, int hkv, int nb_max) {
 template <int D, int G>
 int launch_select(const SelectParams& p, bool qf32, bool kbf16, dim3 grid, hipStream_t st) {
   const size_t lds = (size_t)p.lds_scores * sizeof(float);
-  if (qf32) {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, true>), grid, dim3(kSelThreads), lds, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, true, false>), grid, dim3(kSelThreads), lds, st, p);
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kSelThreads), lds, st, p); };
+  if (p.quest) {
+    if (qf32) kbf16 ? go(ia_condition_block_select_topk<D, G, true, true, true>)
+                    : go(ia_condition_block_select_topk<D, G, true, false, true>);
+    else kbf16 ? go(ia_condition_block_select_topk<D, G, false, true, true>)
+               : go(ia_condition_block_select_topk<D, G, false, false, true>);
   } else {
-    if (kbf16) hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, true>), grid, dim3(kSelThreads), lds, st, p);
-    else hipLaunchKernelGGL((ia_condition_block_select_topk<D, G, false, false>), grid, dim3(kSelThreads), lds, st, p);
+    if (qf32) kbf16 ? go(ia_condition_block_select_topk<D, G, true, true, false>)
+                    : go(ia_condition_block_select_topk<D, G, true, false, false>);
+    else kbf16 ? go(ia_condition_block_select_topk<D, G, false, true, false>)
+               : go(ia_condition_block_select_topk<D, G, false, false, false>);
   }
   return check_launch("select_topk");
 }
 
 }  // namespace
 
-int run_topk_scores(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
-                    int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens, int32_t block_size,
-                    int32_t nb_max, float* scores, const TopkPlanArgs& plan, hipStream_t st) {
-  const int G = shape->n_q_heads / shape->n_kv_heads;
-  const int D = shape->head_dim;
-  SelectParams p{};
-  p.q = q;
-  p.q_batch_stride = shape->q_batch_stride;
-  p.q_row_stride = shape->q_row_stride;
-  p.k_bar = k_bar;
-  p.kb_batch_stride = kbar_batch_stride;
-  p.kb_head_stride = kbar_head_stride;
-  p.seq_lens = seq_lens;
-  p.block_size = block_size;
-  p.nb_max = nb_max;
-  p.scores = scores;
-  p.n_kv_heads = shape->n_kv_heads;
-  p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
-  p.k = plan.k;
-  p.k_per_seq = plan.k_per_seq;
-  p.forced_first = plan.forced_first;
-  p.forced_last = plan.forced_last;
-  p.forced_in_k = plan.forced_in_k;
-  p.k_cap = plan.k_cap;
-  p.plan = plan.entries;
-  p.plan_grid = plan.grid;
-  p.plan_budget = plan.budget;
-  p.plan_max_items = plan.max_items;
-  p.n_rows = plan.n_rows;
-  const dim3 grid(1 + (nb_max + kScoreBlocksPerWg - 1) / kScoreBlocksPerWg, shape->n_kv_heads, shape->batch);
-  const bool qf32 = shape->q_dtype == IA_F32;
-  const bool kbf16 = k_bar_dtype == IA_BF16;
-#define IA_SC(DD, GG) \
-  if (D == DD && G == GG) { launch_scores<DD, GG>(p, qf32, kbf16, grid, st); return check_launch("topk scores"); }
-  IA_SC(128, 4) IA_SC(128, 8) IA_SC(128, 2) IA_SC(128, 1)
-  IA_SC(64, 4) IA_SC(64, 8) IA_SC(64, 2) IA_SC(64, 1)
-#undef IA_SC
-  return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination");
+// Checks a block-keys descriptor and returns the score scale: 1 / (G sqrt(D)) for the
+// mean-key score, 1 / G for the Quest score (CBG/methods/quest.py:97-101 takes the
+// group mean and no 1/sqrt(D)).
+int check_block_keys(const ia_block_keys* keys, int G, int D, float* score_scale) {
+  if (!keys) return fail(IA_ERR_INVALID, "block keys are null");
+  if (keys->dtype != IA_F32 && keys->dtype != IA_BF16) return fail(IA_ERR_INVALID, "key dtype must be IA_F32 or IA_BF16");
+  const int eb = keys->dtype == IA_BF16 ? 2 : 4;
+  if ((keys->batch_stride * eb) % 16 || (keys->head_stride * eb) % 16 || keys->batch_stride < 0 || keys->head_stride < 0)
+    return fail(IA_ERR_INVALID, "key rows must be 16-byte aligned");
+  const void* ptrs[2] = {nullptr, nullptr};
+  if (keys->score == IA_SCORE_MEAN_KEY) {
+    ptrs[0] = keys->k_bar;
+    ptrs[1] = keys->k_bar;
+    *score_scale = 1.0f / ((float)G * std::sqrt((float)D));
+  } else if (keys->score == IA_SCORE_QUEST) {
+    ptrs[0] = keys->k_max;
+    ptrs[1] = keys->k_min;
+    *score_scale = 1.0f / (float)G;
+  } else {
+    return fail(IA_ERR_INVALID, "score must be IA_SCORE_MEAN_KEY or IA_SCORE_QUEST");
+  }
+  for (const void* ptr : ptrs) {
+    if (!ptr) return fail(IA_ERR_INVALID, "the score's key rows must be non-null (k_bar, or k_max and k_min)");
+    if (reinterpret_cast<uintptr_t>(ptr) % 16) return fail(IA_ERR_INVALID, "key rows must be 16-byte aligned");
+  }
+  return IA_OK;
 }
 
 }  // namespace ia
@@ -394,8 +265,7 @@ size_t ia_select_topk_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t 
   return ia::select_ws_size(batch, n_kv_heads, nb_max);
 }
 
-int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_bar, int32_t k_bar_dtype,
-                   int64_t kbar_batch_stride, int64_t kbar_head_stride, const int32_t* seq_lens,
+int ia_select_topk(const ia_decode_shape* shape, const void* q, const ia_block_keys* keys, const int32_t* seq_lens,
                    int32_t block_size, int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,
                    int32_t forced_last, int32_t forced_in_k, int32_t* idx, int32_t k_cap, int32_t* n_sel,
                    float* scores, void* workspace, size_t workspace_bytes, void* stream) {
@@ -408,25 +278,27 @@ int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_ba
   if (D != 64 && D != 128) return fail(IA_ERR_UNSUPPORTED, "head_dim must be 64 or 128");
   if (G != 1 && G != 2 && G != 4 && G != 8) return fail(IA_ERR_UNSUPPORTED, "GQA group size must be 1, 2, 4 or 8");
   if (shape->q_dtype != IA_F32 && shape->q_dtype != IA_BF16) return fail(IA_ERR_INVALID, "q dtype");
-  if (k_bar_dtype != IA_F32 && k_bar_dtype != IA_BF16) return fail(IA_ERR_INVALID, "k_bar dtype must be IA_F32 or IA_BF16");
-  if (!q || !k_bar || !seq_lens || !idx || !n_sel) return fail(IA_ERR_INVALID, "null pointer argument");
+  float score_scale = 0.f;
+  int rc = check_block_keys(keys, G, D, &score_scale);
+  if (rc) return rc;
+  if (!q || !seq_lens || !idx || !n_sel) return fail(IA_ERR_INVALID, "null pointer argument");
   if (block_size <= 0) return fail(IA_ERR_INVALID, "block_size must be positive");
   if (nb_max < 0 || k < 0 || forced_first < 0 || forced_last < 0 || k_cap <= 0)
     return fail(IA_ERR_INVALID, "nb_max, k, forced_* must be >= 0 and k_cap > 0");
-  const int eb = k_bar_dtype == IA_BF16 ? 2 : 4;
-  if ((kbar_batch_stride * eb) % 16 || (kbar_head_stride * eb) % 16 || reinterpret_cast<uintptr_t>(k_bar) % 16)
-    return fail(IA_ERR_INVALID, "k_bar rows must be 16-byte aligned");
   const size_t need = select_ws_size(shape->batch, shape->n_kv_heads, nb_max);
   if (!scores && nb_max > kMaxLdsScores && (!workspace || workspace_bytes < need))
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) + " bytes");
   if (shape->batch == 0) return IA_OK;
+  const bool quest = keys->score == IA_SCORE_QUEST;
   SelectParams p{};
   p.q = q;
   p.q_batch_stride = shape->q_batch_stride;
   p.q_row_stride = shape->q_row_stride;
-  p.k_bar = k_bar;
-  p.kb_batch_stride = kbar_batch_stride;
-  p.kb_head_stride = kbar_head_stride;
+  p.k_bar = quest ? keys->k_max : keys->k_bar;
+  p.k_min = keys->k_min;
+  p.quest = quest;
+  p.kb_batch_stride = keys->batch_stride;
+  p.kb_head_stride = keys->head_stride;
   p.seq_lens = seq_lens;
   p.block_size = block_size;
   p.nb_max = nb_max;
@@ -441,12 +313,12 @@ int ia_select_topk(const ia_decode_shape* shape, const void* q, const void* k_ba
   // scores go to global memory when asked for, or when a row does not fit in LDS
   p.scores = scores ? scores : (nb_max > kMaxLdsScores ? reinterpret_cast<float*>(workspace) : nullptr);
   p.n_kv_heads = shape->n_kv_heads;
-  p.score_scale = 1.0f / ((float)G * std::sqrt((float)D));
+  p.score_scale = score_scale;
   p.lds_scores = nb_max <= kMaxLdsScores ? nb_max : 0;
   dim3 grid(shape->n_kv_heads, shape->batch);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool qf32 = shape->q_dtype == IA_F32;
-  const bool kbf16 = k_bar_dtype == IA_BF16;
+  const bool kbf16 = keys->dtype == IA_BF16;
 #define IA_SEL(DD, GG) \
   if (D == DD && G == GG) return launch_select<DD, GG>(p, qf32, kbf16, grid, st);
   IA_SEL(128, 4) IA_SEL(128, 8) IA_SEL(128, 2) IA_SEL(128, 1)

@@ -17,8 +17,8 @@
 //         stopping as soon as the threshold bin is taken whole;
 //   * an ordered compaction (one block-wide scan of per-thread counts over
 //     contiguous index ranges) emits the chosen block ids in ascending order.
-// The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103
-// with the mean key (k_bar) as the block representative.
+// The rule is the group-mean score + torch.topk of CBG/methods/quest.py:91-103,
+// with the mean key (k_bar) or Quest's page bound (k_max, k_min) scoring a block.
 #pragma once
 
 #include "ia_common.hpp"
@@ -51,6 +51,32 @@ __device__ __forceinline__ float block_score(const u32* w, const float* qm, floa
   } else {
 #pragma unroll
     for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], __uint_as_float(w[e]), a);
+  }
+  return row16_sum(a) * score_scale;
+}
+
+// Quest score of one block (CBG/methods/quest.py:97-101): the group mean of
+// sum_d max(q_gd k_max_d, q_gd k_min_d), which, since k_max >= k_min, equals
+// (qa . k_max + qb . k_min) / G with qa = sum_g max(q_g, 0), qb = sum_g min(q_g, 0)
+// (score_scale = 1 / G).  Key rows as for block_score.
+template <int DPL, bool KBF16>
+__device__ __forceinline__ float block_score_quest(const u32* wx, const u32* wn, const float* qa, const float* qb,
+                                                   float score_scale) {
+  float a = 0.f;
+  if constexpr (KBF16) {
+#pragma unroll
+    for (int e = 0; e < DPL / 2; ++e) {
+      a = fmaf(qa[2 * e], bf16_lo(wx[e]), a);
+      a = fmaf(qb[2 * e], bf16_lo(wn[e]), a);
+      a = fmaf(qa[2 * e + 1], bf16_hi(wx[e]), a);
+      a = fmaf(qb[2 * e + 1], bf16_hi(wn[e]), a);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      a = fmaf(qa[e], __uint_as_float(wx[e]), a);
+      a = fmaf(qb[e], __uint_as_float(wn[e]), a);
+    }
   }
   return row16_sum(a) * score_scale;
 }
@@ -196,7 +222,7 @@ __device__ __forceinline__ void topk_stage(TopkLds<NT>& L, u32 kmx, u32 kmn_inv)
 // of chosen blocks (clamped to k_cap).  STAGED: the caller ran topk_stage and a
 // workgroup barrier (the first pass over the row is skipped).
 template <int NT, bool STAGED = false, typename KeyAt, typename Emit>
-__device__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule& rule, Emit emit) {
+__device__ __forceinline__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb, const TopkRule& rule, Emit emit) {
   constexpr int kWv = NT / 64;
   const int wave = threadIdx.x >> 6;
   const TopkForced is_forced(rule, nb);

@@ -229,25 +229,61 @@ def append_kv(pool_k, pool_v, block_table, seq_lens, k_new, v_new):
 
 # --------------------------------------------------------------------------- top-k selection
 
+SCORES = {"mean": N.IA_SCORE_MEAN_KEY, "quest": N.IA_SCORE_QUEST}
+
+
+def _block_keys(k_bar, score):
+    """C-ABI block keys.  ``score="mean"``: ``k_bar [B, Hkv, nb_max, D]``; ``"quest"``:
+    ``k_bar = (k_max, k_min)``, both ``[B, Hkv, nb_max, D]`` of one dtype and layout.
+    Returns ``(BlockKeys, (B, Hkv, nb_max, D), dtype, keepalive)``."""
+    if score not in SCORES:
+        raise ValueError(f"score must be one of {sorted(SCORES)}, got {score!r}")
+    arrays = tuple(k_bar) if score == "quest" else (k_bar,)
+    if score == "quest" and len(arrays) != 2:
+        raise ValueError("score='quest' takes k_bar=(k_max, k_min)")
+    ref = arrays[0]
+    _require_cuda(*arrays)
+    for t in arrays:
+        if t.dim() != 4 or t.stride(3) != 1 or t.stride(2) != t.shape[3]:
+            raise ValueError("block keys must be [B, Hkv, nb_max, D] with contiguous blocks")
+        if t.shape != ref.shape or t.stride() != ref.stride() or t.dtype != ref.dtype:
+            raise ValueError("k_max and k_min must share shape, strides and dtype")
+    keys = N.BlockKeys()
+    keys.score = SCORES[score]
+    keys.dtype = _code(ref.dtype, "block keys")
+    if score == "quest":
+        keys.k_max, keys.k_min = arrays[0].data_ptr(), arrays[1].data_ptr()
+    else:
+        keys.k_bar = ref.data_ptr()
+    keys.batch_stride, keys.head_stride = int(ref.stride(0)), int(ref.stride(1))
+    return keys, tuple(int(x) for x in ref.shape), ref.dtype, arrays
+
+
+def set_wait_limit(ticks):
+    """Bound (100 MHz clock ticks) of every wait between the workgroups of a fused
+    top-k call; a negative value restores the default.  Returns the previous bound."""
+    return int(N.lib().ia_set_wait_limit(int(ticks)))
+
 def select_blocks_topk(q, k_bar, seq_lens, k, *, block_size, forced_first=0, forced_last=0,
-                       forced_in_k=False, k_cap=None, k_per_seq=None, return_scores=False, workspace=None):
+                       forced_in_k=False, k_cap=None, k_per_seq=None, return_scores=False, score="mean",
+                       workspace=None):
     """Top-k block selection per (sequence, kv head).
 
-    ``q [B, Hq, D]``, ``k_bar [B, Hkv, nb_max, D]`` (bf16/fp32 summaries).  Score =
-    group-mean ``q . k_bar / sqrt(D)`` (CBG/methods/quest.py:91-103).  Returns
-    ``(idx [B, Hkv, k_cap] int32, n_sel [B, Hkv] int32[, scores [B, Hkv, nb_max] f32])``;
-    ``idx[b, h, :n_sel[b, h]]`` are the chosen blocks in ascending order (forced first
-    ``forced_first`` / last ``forced_last`` blocks included; ``forced_in_k`` counts them
-    inside ``k``).  Ties at the k-th score go to the lower block index.  ``k_per_seq``
-    (int32 ``[B]`` on the device) overrides ``k`` per sequence; ``k_cap`` must then cover
-    its largest entry plus the forced blocks."""
-    _require_cuda(q, k_bar, seq_lens)
-    if k_bar.dim() != 4 or k_bar.stride(3) != 1 or k_bar.stride(2) != k_bar.shape[3]:
-        raise ValueError("k_bar must be [B, Hkv, nb_max, D] with contiguous blocks")
-    b, hkv, nb_max, d = (int(s) for s in k_bar.shape)
+    ``q [B, Hq, D]``.  ``score="mean"``: ``k_bar [B, Hkv, nb_max, D]`` (bf16/fp32
+    summaries), score = group-mean ``q . k_bar / sqrt(D)``; ``score="quest"``:
+    ``k_bar = (k_max, k_min)``, score = group-mean ``sum_d max(q_d k_max_d, q_d k_min_d)``
+    (CBG/methods/quest.py:91-103).  Returns ``(idx [B, Hkv, k_cap] int32, n_sel [B, Hkv]
+    int32[, scores [B, Hkv, nb_max] f32])``; ``idx[b, h, :n_sel[b, h]]`` are the chosen
+    blocks in ascending order (forced first ``forced_first`` / last ``forced_last``
+    blocks included; ``forced_in_k`` counts them inside ``k``).  Ties at the k-th score
+    go to the lower block index.  ``k_per_seq`` (int32 ``[B]`` on the device) overrides
+    ``k`` per sequence; ``k_cap`` must then cover its largest entry plus the forced
+    blocks."""
+    keys, (b, hkv, nb_max, d), _, keep = _block_keys(k_bar, score)
+    _require_cuda(q, seq_lens)
     sh = _decode_shape(q, hkv)
     if q.shape[0] != b or q.shape[2] != d:
-        raise ValueError("q and k_bar disagree on batch or head_dim")
+        raise ValueError("q and the block keys disagree on batch or head_dim")
     _check_i32(seq_lens, "seq_lens", (b,))
     if k < 0 or forced_first < 0 or forced_last < 0:
         raise ValueError("k and forced block counts must be >= 0")
@@ -269,12 +305,12 @@ def select_blocks_topk(q, k_bar, seq_lens, k, *, block_size, forced_first=0, for
     ws_bytes = lib.ia_select_topk_workspace_size(b, hkv, nb_max)
     ws = _scratch(workspace if workspace is not None else {}, "topk_scratch", ws_bytes, dev)
     rc = lib.ia_select_topk(
-        sh, q.data_ptr(), k_bar.data_ptr(), _code(k_bar.dtype, "k_bar"), int(k_bar.stride(0)),
-        int(k_bar.stride(1)), seq_lens.data_ptr(), int(block_size), nb_max, int(k),
+        sh, q.data_ptr(), keys, seq_lens.data_ptr(), int(block_size), nb_max, int(k),
         None if k_per_seq is None else k_per_seq.data_ptr(), int(forced_first),
         int(forced_last), int(bool(forced_in_k)), idx.data_ptr(), k_cap, n_sel.data_ptr(),
         None if scores is None else scores.data_ptr(), ws.data_ptr(), ws.numel(), _stream(q))
     N.check(rc)
+    del keep
     if return_scores:
         return idx, n_sel, scores
     return idx, n_sel
@@ -451,16 +487,18 @@ FUSED_MAX_K_CAP = 512
 
 def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, block_size, forced_first=0,
                        forced_last=0, forced_in_k=False, k_cap=None, k_per_seq=None, scale=None, scales=None,
-                       out=None, out_dtype=None, return_selection=False, workspace=None):
+                       out=None, out_dtype=None, return_selection=False, score="mean", workspace=None):
     """One decode-attention layer call of the top-k path: the selection of
-    ``select_blocks_topk`` followed by ``sparse_paged_decode``.  Up to 4096 blocks per
-    sequence and ``k_cap <= 512`` it runs fused (``ia_sparse_topk_decode``: a
-    many-workgroup scorer, then the finalize selecting in its prologue); beyond that
-    as the two calls.  With ``return_selection`` returns ``(out, idx, n_sel)``."""
-    _require_cuda(q, k_bar, seq_lens)
-    if k_bar.dim() != 4 or k_bar.stride(3) != 1 or k_bar.stride(2) != k_bar.shape[3]:
-        raise ValueError("k_bar must be [B, Hkv, nb_max, D] with contiguous blocks")
-    b, hkv, nb_max, d = (int(s_) for s_ in k_bar.shape)
+    ``select_blocks_topk`` (``score`` and ``k_bar`` as there) followed by
+    ``sparse_paged_decode``.  Up to 4096 blocks per sequence and ``k_cap <= 512`` it is
+    one launch (``ia_sparse_topk_decode``: each (sequence, kv head) row's items score
+    their share of the blocks, exchange scores, select, stream their share of the
+    chosen blocks and merge); beyond that the two calls.  The launch's workspace
+    (``workspace[("topk_decode_scratch", *shape)]``, one per call shape) is zero-filled
+    when it is created and must not be shared by overlapping calls.  With ``return_selection`` returns
+    ``(out, idx, n_sel)``."""
+    keys, (b, hkv, nb_max, d), _, keep_k = _block_keys(k_bar, score)
+    _require_cuda(q, seq_lens)
     if k < 0 or forced_first < 0 or forced_last < 0:
         raise ValueError("k and forced block counts must be >= 0")
     if k_per_seq is not None:
@@ -474,16 +512,16 @@ def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, bl
     if nb_max > FUSED_MAX_BLOCKS or k_cap > FUSED_MAX_K_CAP:
         idx, n_sel = select_blocks_topk(q, k_bar, seq_lens, k, block_size=block_size, forced_first=forced_first,
                                         forced_last=forced_last, forced_in_k=forced_in_k, k_cap=k_cap,
-                                        k_per_seq=k_per_seq, workspace=workspace)
+                                        k_per_seq=k_per_seq, score=score, workspace=workspace)
         res = sparse_paged_decode(q, pool_k, pool_v, block_table, seq_lens, idx, n_sel, block_size=block_size,
                                   scale=scale, scales=scales, out=out, out_dtype=out_dtype, workspace=workspace)
         return (res, idx, n_sel) if return_selection else res
     kv, keep = paged_kv(pool_k, pool_v, block_table, scales)
     if int(pool_k.shape[1]) != hkv or int(pool_k.shape[3]) != d:
-        raise ValueError("k_bar and the pool disagree on Hkv or head_dim")
+        raise ValueError("the block keys and the pool disagree on Hkv or head_dim")
     sh = _decode_shape(q, hkv)
     if q.shape[0] != b or q.shape[2] != d:
-        raise ValueError("q and k_bar disagree on batch or head_dim")
+        raise ValueError("q and the block keys disagree on batch or head_dim")
     _check_i32(seq_lens, "seq_lens", (b,))
     if block_table is not None and block_table.shape[0] != b:
         raise ValueError("block_table rows must match the batch")
@@ -497,16 +535,18 @@ def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, bl
     lib = N.lib()
     g = int(q.shape[1]) // hkv
     ws_bytes = lib.ia_sparse_topk_decode_workspace_size(b, hkv, g, d, nb_max, k_cap)
-    ws = _scratch(workspace if workspace is not None else {}, "topk_decode_scratch", ws_bytes, dev)
+    # the launch keeps per-row counts in its workspace from call to call: one
+    # zero-filled buffer per call shape
+    ws = _scratch(workspace if workspace is not None else {}, ("topk_decode_scratch", b, hkv, g, d, nb_max, k_cap),
+                  ws_bytes, dev)
     rc = lib.ia_sparse_topk_decode(
-        sh, q.data_ptr(), kv, seq_lens.data_ptr(), k_bar.data_ptr(), _code(k_bar.dtype, "k_bar"),
-        int(k_bar.stride(0)), int(k_bar.stride(1)), int(block_size), nb_max, int(k),
+        sh, q.data_ptr(), kv, seq_lens.data_ptr(), keys, int(block_size), nb_max, int(k),
         None if k_per_seq is None else k_per_seq.data_ptr(), int(forced_first), int(forced_last),
         int(bool(forced_in_k)), k_cap, scale, out.data_ptr(), _code(out.dtype, "out"),
         None if idx is None else idx.data_ptr(), None if n_sel is None else n_sel.data_ptr(), ws.data_ptr(),
         ws.numel(), _stream(q))
     N.check(rc)
-    del keep
+    del keep, keep_k
     return (out, idx, n_sel) if return_selection else out
 
 

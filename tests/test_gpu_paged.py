@@ -449,3 +449,82 @@ def test_sparse_decode_with_representatives(dt, device):
                                   host["v_bar"][b, :, :nb], sel, np.zeros((hkv, 0, d), np.float32),
                                   np.zeros((hkv, 0, d), np.float32), emulate_bf16=(dt == "bf16"))
         np.testing.assert_allclose(got[b], ref[:, :, 0].reshape(hq, d), atol=TOL[dt], rtol=0)
+
+
+@pytest.mark.parametrize("c", CASES, ids=IDS)
+def test_quest_score_selection_and_decode(c, device):
+    """The Quest page score (CBG/methods/quest.py:97-101) on the device: scores equal
+    the oracle's (float64, 1e-5), indices equal the oracle's top-k of them (near-tie
+    rule), the fused layer call equals select + decode bit for bit, and the output
+    equals exact attention over the chosen blocks."""
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    k, ff, fl, in_k = sel
+    announce(f"quest score {name}")
+    case = _build(c)
+    dev = to_dev(case, device, _torch_dtype(dt))
+    nb_max = max(math.ceil(L / block) for L in lens)
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max, full=True)
+    keys = (summ["k_max"], summ["k_min"])
+    kw = dict(block_size=block, forced_first=ff, forced_last=fl, forced_in_k=in_k, score="quest")
+    idx, n_sel, scores = ia.select_blocks_topk(dev["q"], keys, dev["seq_lens"], k, return_scores=True, **kw)
+    ref = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block)
+    out, idx2, n_sel2 = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"],
+                                              dev["seq_lens"], keys, k, return_selection=True, workspace={}, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(n_sel2, n_sel) and torch.equal(out, ref)
+    g = hq // hkv
+    got = out.float().cpu().numpy()
+    for i, L in enumerate(lens):
+        nb = math.ceil(L / block)
+        kx = summ["k_max"][i, :, :nb].double().cpu().numpy()
+        kn = summ["k_min"][i, :, :nb].double().cpu().numpy()
+        sc = S.quest_block_scores(case["q"][i], kx, kn, g)
+        np.testing.assert_allclose(scores[i, :, :nb].cpu().numpy(), sc, rtol=1e-5, atol=1e-5)
+        chosen = []
+        for h in range(hkv):
+            n = int(n_sel[i, h])
+            check_indices(idx[i, h].cpu().numpy(), n, sc[h], nb, k, ff, fl, in_k)
+            assert torch.equal(idx2[i, h, :n], idx[i, h, :n])
+            chosen.append(idx[i, h, :n].cpu().numpy())
+        exp = A.sparse_decode(case["q"][i], case["k"][i], case["v"][i], chosen, block, p_bf16=dt == "bf16")
+        assert np.abs(got[i] - exp).max() <= TOL[dt]
+
+
+@pytest.mark.parametrize("name", ["c2_small", "c4_small", "ragged_b3", "g8_d64"])
+def test_fused_handoff_fallback_is_exact(name, device):
+    """With a wait bound of 0 every item that finds a partner's scores missing scores
+    that range itself: the result (selection and output) equals the waiting run's bit
+    for bit.  One workspace serves calls on different queries back to back, so flags
+    left set by a call would show up as a wrong selection in the next."""
+    c = CASES[IDS.index(name)]
+    _, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    k, ff, fl, in_k = sel
+    announce(f"fused hand-off fallback {name}")
+    case = _build(c)
+    dev = to_dev(case, device, _torch_dtype(dt))
+    nb_max = max(math.ceil(L / block) for L in lens)
+    kb_dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max, k_bar_dtype=kb_dtype)
+    kw = dict(block_size=block, forced_first=ff, forced_last=fl, forced_in_k=in_k)
+    gen = torch.Generator(device=device).manual_seed(5)
+    qs = [dev["q"]] + [torch.randn(dev["q"].shape, device=device, generator=gen).to(dev["q"].dtype) for _ in range(2)]
+    refs = []
+    for q in qs:
+        idx, n_sel = ia.select_blocks_topk(q, summ["k_bar"], dev["seq_lens"], k, **kw)
+        refs.append(ia.sparse_paged_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                           idx, n_sel, block_size=block).clone())
+    ws = {}
+    previous = ia.set_wait_limit(0)
+    try:
+        got0 = [ia.sparse_topk_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                      summ["k_bar"], k, workspace=ws, **kw).clone() for q in qs]
+    finally:
+        ia.set_wait_limit(previous)
+    got = [ia.sparse_topk_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                 summ["k_bar"], k, workspace=ws, **kw).clone() for q in qs]
+    torch.cuda.synchronize()
+    for r, a, b_ in zip(refs, got0, got):
+        assert torch.equal(a, r) and torch.equal(b_, r)

@@ -21,9 +21,9 @@ repeated k_bar rows so that exact ties are frequent:
 * ``far``: random rows plus a few scaled by 1e6 (a huge range, most candidates in
   one bucket);
 * ``random``: plain random rows (the bucket fast path).
-Both the standalone selector and the fused layer call (selection in the finalize
-prologue) are checked; the standalone one also on 20000-block rows, whose ties sit
-in the second compaction chunk.
+Both the standalone selector (one workgroup) and the fused layer call (one wave of
+the finalize prologue) are checked; the standalone one also on 20000-block rows,
+whose ties sit in the second compaction chunk, the fused one on 4000-block rows.
 """
 
 import math
@@ -130,3 +130,27 @@ def test_selection_rule_long_rows(pattern, device):
                                                forced_last=rule[2], return_scores=True)
     torch.cuda.synchronize()
     _check(idx[0].cpu().numpy(), n_sel[0].cpu().numpy(), scores[0].float().cpu().numpy(), nb, rule)
+
+
+@pytest.mark.parametrize("pattern", ["dup5", "zero", "crowd", "crowd40", "random"])
+def test_fused_selection_rule_4000(pattern, device):
+    """The fused call's one-wave selection on 4000-block rows (63 chunks of 64)."""
+    announce(f"fused selection rule 4000 {pattern}")
+    rng = np.random.default_rng(7 + PATTERNS.index(pattern))
+    nb = 4000
+    L = nb * BLOCK - 3
+    q, kb = _rows(pattern, nb, rng)
+    q_t, kb_t = _to_dev(q, kb, device)
+    seq = torch.tensor([L], device=device, dtype=torch.int32)
+    rule = (300, 2, 3, False)
+    _, _, scores = ia.select_blocks_topk(q_t, kb_t, seq, rule[0], block_size=BLOCK, forced_first=rule[1],
+                                         forced_last=rule[2], return_scores=True)
+    n_pages = math.ceil(L / PAGE)
+    pool_k = torch.randn((n_pages, HKV, PAGE, D), device=device, dtype=torch.bfloat16)
+    pool_v = torch.randn((n_pages, HKV, PAGE, D), device=device, dtype=torch.bfloat16)
+    table = torch.arange(n_pages, device=device, dtype=torch.int32)[None]
+    _, idx_f, n_f = ia.sparse_topk_decode(q_t, pool_k, pool_v, table, seq, kb_t, rule[0], block_size=BLOCK,
+                                          forced_first=rule[1], forced_last=rule[2], return_selection=True,
+                                          workspace={})
+    torch.cuda.synchronize()
+    _check(idx_f[0].cpu().numpy(), n_f[0].cpu().numpy(), scores[0].float().cpu().numpy(), nb, rule)

@@ -39,6 +39,8 @@ def test_struct_layouts_match_the_header():
     assert ctypes.sizeof(N.BlockSummaries) == 8 * 4 + 4 * 4 + 8 * 3 + 4 * 2
     # ia_suffix_kv: 2 pointers, 6 int64, pointer, 2 int32
     assert ctypes.sizeof(N.SuffixKV) == 8 * 2 + 8 * 6 + 8 + 4 * 2
+    # ia_block_keys: 2 int32, 3 pointers, 2 int64
+    assert ctypes.sizeof(N.BlockKeys) == 4 * 2 + 8 * 3 + 8 * 2
 
 
 def test_workspace_sizes_are_consistent():
@@ -62,11 +64,23 @@ def test_invalid_arguments_are_rejected_without_launching():
     sh.n_q_heads = 32
     sh.n_kv_heads = 8
     sh.head_dim = 96
-    rc = lib.ia_select_topk(sh, None, None, N.IA_BF16, 0, 0, None, 64, 8, 4, None, 0, 0, 0, None, 4, None, None,
-                            None, 0, None)
+    keys = N.BlockKeys(score=N.IA_SCORE_MEAN_KEY, dtype=N.IA_BF16)
+    rc = lib.ia_select_topk(sh, None, keys, None, 64, 8, 4, None, 0, 0, 0, None, 4, None, None, None, 0, None)
     assert rc != 0
     with pytest.raises(ValueError):
         N.check(rc)
+    # an unknown score, and a Quest score without its k_max / k_min rows
+    sh.head_dim = 128
+    for bad in (N.BlockKeys(score=7, dtype=N.IA_BF16, k_bar=256),
+                N.BlockKeys(score=N.IA_SCORE_QUEST, dtype=N.IA_BF16, k_bar=256)):
+        rc = lib.ia_select_topk(sh, 256, bad, 256, 64, 8, 4, None, 0, 0, 0, 256, 4, 256, None, None, 0, None)
+        assert rc == N.IA_ERR_INVALID, lib.ia_last_error()
+        rc = lib.ia_sparse_topk_decode(sh, 256, kv, 256, bad, 64, 8, 4, None, 0, 0, 0, 4, 1.0, 256, N.IA_BF16, None,
+                                       None, None, 0, None)
+        assert rc == N.IA_ERR_INVALID
+    previous = lib.ia_set_wait_limit(5)
+    assert lib.ia_set_wait_limit(-1) == 5 and previous > 0
+    assert lib.ia_set_wait_limit(-1) == previous
     rc = lib.ia_build_block_summaries(kv, None, 1, 8, 128, 64, 4, None, 1, None, 1, None, None, 1, None, None, None,
                                       None)
     assert rc == N.IA_ERR_INVALID

@@ -338,15 +338,18 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
  * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  The workspace
  * (ia_sparse_topk_decode_workspace_size bytes) must be zero-filled before its first
  * use and then left to the library, and used with one set of (batch, n_kv_heads,
- * group, head_dim, nb_max, k_cap) (zero-fill it again for another): it carries a
- * per-row call count and finished-item count from call to call.  Calls that share
+ * group, head_dim, nb_max, k_cap, block_size) (zero-fill it again for another): it
+ * carries a per-row call count and finished-item count from call to call.  Its size
+ * follows the device's resident workgroups (one split-K slot per workgroup): size
+ * it with the device current on which the call runs.  Calls that share
  * a workspace must not overlap.  Replaces the selection +
  * finalize pair of one decode step, _select_prompt_blocks_triton +
  * _condition_block_decode_output_fused_triton (CBT/core.py:701-744, :1035-1155),
  * for the BASELINE's top-k rule.
  */
 IA_API size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
-                                                   int32_t head_dim, int32_t nb_max, int32_t k_cap);
+                                                   int32_t head_dim, int32_t nb_max, int32_t k_cap,
+                                                   int32_t block_size);
 IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
                                  const int32_t* seq_lens, const ia_block_keys* keys, int32_t block_size,
                                  int32_t nb_max, int32_t k, const int32_t* k_per_seq, int32_t forced_first,

@@ -134,7 +134,7 @@ SIGNATURES = {
          _P, _P, _P],
     ),
     "ia_append_kv": (ctypes.c_int, [ctypes.POINTER(PagedKV), _P, _P, _I64, _I64, _P, _I32, _I32, _I32, _P]),
-    "ia_sparse_topk_decode_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "ia_sparse_topk_decode_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "ia_sparse_topk_decode": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, ctypes.POINTER(BlockKeys), _I32, _I32, _I32,

@@ -189,18 +189,34 @@ int run_decode(bool sparse, const ia_decode_shape* shape, const void* q, const i
   return dispatch_decode(p, kv->dtype, D, G, src, dim3(grid), st, nullptr);
 }
 
-// Fused top-k decode workspace: one 256-byte line per row first (the row's
-// finished-partial count, zero between calls, and its epoch), then the published
-// score entries [row, nb_max] (8 bytes each) and the split-K partials.
-struct FusedWs {
-  size_t sbuf, decode, total;
-};
-FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap) {
+}  // namespace
+
+// Most workgroups a fused launch over `rows` rows may use: the largest resident count
+// of its kernel over the kv dtypes, or rows x ceil(s_cap / t_cap) when LDS bounds
+// force small items (balanced_grid's rule).
+int64_t fused_grid_bound(int64_t rows, int g, int d, int k_cap, int block_size) {
+  int resident = 0;
+  const DecodeParams none{};
+  for (auto run : {dispatch_bf16, dispatch_fp8, dispatch_f32}) {
+    int r = 0;
+    if (run(none, d, g, kSrcTopkFused, dim3(1), nullptr, &r) == IA_OK) resident = std::max(resident, r);
+  }
+  if (resident <= 0) resident = 1024;
+  const int nsub_u = std::max(block_size / 16, 1);
+  const int64_t t_cap = plan_t_cap(nsub_u);
+  const int64_t s_cap = (int64_t)std::max(k_cap, 1) * nsub_u;
+  return std::max<int64_t>(std::max<int64_t>(resident, rows), rows * ((s_cap + t_cap - 1) / t_cap));
+}
+
+FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size) {
   const int64_t rows = (int64_t)batch * hkv;
   FusedWs L;
+  L.slots = fused_grid_bound(rows, g, d, k_cap, block_size);
   L.sbuf = align_up((size_t)rows * kFlagStride * 4, 256);
-  L.decode = align_up(L.sbuf + (size_t)rows * std::max(nb_max, 1) * 8, 256);
-  L.total = align_up(L.decode + decode_ws_size(batch, hkv, g, d, units_cap_items(k_cap)), 256);
+  L.part_ml = align_up(L.sbuf + (size_t)rows * std::max(nb_max, 1) * 8, 256);
+  L.part_acc = align_up(L.part_ml + (size_t)L.slots * g * 2 * 4, 256);
+  L.part_n = align_up(L.part_acc + (size_t)L.slots * g * d * 4, 256);
+  L.total = align_up(L.part_n + (size_t)rows * 4, 256);
   return L;
 }
 
@@ -229,7 +245,7 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
     return fail(IA_ERR_UNSUPPORTED, "fused top-k decode takes nb_max <= " + std::to_string(kFusedMaxBlocks) +
                                         " and k_cap <= " + std::to_string(kMaxUnitsPerItem) +
                                         "; use ia_select_topk + ia_sparse_paged_decode");
-  const FusedWs L = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap);
+  const FusedWs L = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, block_size);
   if (!workspace || workspace_bytes < L.total)
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(L.total) + " bytes");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
@@ -276,19 +292,21 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   rc = balanced_grid(p, kv->dtype, D, G, kSrcTopkFused, bh, k_cap, block_size / 16, cap_items, st, &grid,
                      &p.plan_budget);
   if (rc) return rc;
+  if (grid > L.slots) return fail(IA_ERR_LAUNCH, "fused grid exceeds its workspace bound");
   p.n_rows = (int)bh;
-  set_decode_ws(p, ws + L.decode, bh, cap_items, G, D);
+  p.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
+  p.part_acc = reinterpret_cast<float*>(ws + L.part_acc);
+  p.part_n = reinterpret_cast<int32_t*>(ws + L.part_n);
   return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(grid), st, nullptr);
 }
 
-}  // namespace
 }  // namespace ia
 
 extern "C" {
 
 size_t ia_sparse_topk_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
-                                            int32_t nb_max, int32_t k_cap) {
-  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1)).total;
+                                            int32_t nb_max, int32_t k_cap, int32_t block_size) {
+  return ia::fused_ws_layout(batch, n_kv_heads, group, head_dim, nb_max, std::max(k_cap, 1), block_size).total;
 }
 
 int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,

@@ -135,8 +135,8 @@ struct DecodeParams {
   int32_t q_f32;     // q is fp32 (else bf16)
   int32_t out_f32;   // out is fp32 (else bf16)
   void* out;
-  float* part_ml;  // [batch*Hkv, max_items, G, 2]
-  float* part_acc; // [batch*Hkv, max_items, G, D]
+  float* part_ml;  // [batch*Hkv, max_items, G, 2] (fused top-k call: [workgroup, G, 2])
+  float* part_acc; // [batch*Hkv, max_items, G, D] (fused top-k call: [workgroup, G, D])
   // balanced sources: items of each (b, h) row, written by the row's item 0 and
   // read by the merge; the plan's workgroup budget and the row count; the fused
   // top-k source reads its plan entries (one per workgroup) from the scorer launch
@@ -425,14 +425,14 @@ __device__ __forceinline__ void merge_combine(int ng, GM gm, GL gl, GA ga, Store
 // (every thread of its workgroup calls it): the row's n partials are read at the
 // coherence point and merged with the merge kernel's merge_group / merge_combine
 // arithmetic, so the output equals the two-step path's bit for bit (which lane
-// computes an output does not change its arithmetic).  Each thread merges outputs
+// computes an output does not change its arithmetic).  The row's partials sit in
+// the slots of its workgroups, slot0 .. slot0 + n - 1.  Each thread merges outputs
 // o = threadIdx.x + kFinThreads k; the first pass's slot loads are issued together
 // with the (m, l) loads that are staged in LDS, so the merge costs one round trip.
 template <int D, int G>
-__device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h, int bh, int n) {
+__device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h, int64_t slot0, int n) {
   constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
   __shared__ float ml_lds[kMaxItemsPerBh][G][2];
-  const int64_t slot0 = (int64_t)bh * p.max_items;
   float acc[kMergeGroups][kMergeGroup];
   auto load_acc = [&](int o) {
 #pragma unroll
@@ -1360,7 +1360,9 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // ---- fold the waves: one (m, l, acc) per item, or the output when the item is alone
   // (a fused call writes its partials through to the coherence point: the row's
   // last item to finish merges them)
-  const int64_t pbase = (int64_t)bh * p.max_items + item;
+  // a fused call's item keeps its partial in its workgroup's slot (the row's items
+  // are consecutive workgroups), others at (row, item)
+  const int64_t pbase = SRC == kSrcTopkFused ? (int64_t)blockIdx.x : (int64_t)bh * p.max_items + item;
   for (int o = threadIdx.x; o < G * D; o += kFinThreads) {
     const int g = o / D;
     float M = kNegInf;
@@ -1411,7 +1413,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         merge_todo[0] = last ? 1u : 0u;
       }
       __syncthreads();
-      if (merge_todo[0]) fused_merge<D, G>(p, b, h, bh, n_items_row);
+      if (merge_todo[0]) fused_merge<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row);
     }
   }
 }
@@ -1736,6 +1738,22 @@ int dispatch_decode(const DecodeParams& p, int kv_dtype, int d, int g, int src, 
                     int* resident);
 int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int64_t bh, int64_t units_max,
                  int nsub_u, int cap_items, hipStream_t st, int* items_out);
+
+// Fused top-k decode workspace: one 256-byte line per row first (the row's
+// finished-partial count, zero between calls, and its epoch), then the published
+// score entries [row, nb_max] (8 bytes each), then the split-K partials, one slot
+// per workgroup ((m, l) [slot, G, 2], acc [slot, G, D]) and the items per row.
+// The part before part_ml carries state from call to call (zero-filled at first).
+struct FusedWs {
+  size_t sbuf, part_ml, part_acc, part_n, total;
+  int64_t slots;
+};
+FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size);
+int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
+                    const ia_block_keys* keys, int32_t block_size, int32_t nb_max, int32_t k,
+                    const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
+                    int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 // Block-keys descriptor check and score scale (select_topk.hip); the hand-off wait
 // bound of the fused top-k call (paged_decode.hip).

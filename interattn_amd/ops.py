@@ -534,11 +534,11 @@ def sparse_topk_decode(q, pool_k, pool_v, block_table, seq_lens, k_bar, k, *, bl
         n_sel = workspace_tensor(workspace, "topk_n_sel", (b, hkv), device=dev, dtype=torch.int32)
     lib = N.lib()
     g = int(q.shape[1]) // hkv
-    ws_bytes = lib.ia_sparse_topk_decode_workspace_size(b, hkv, g, d, nb_max, k_cap)
+    ws_bytes = lib.ia_sparse_topk_decode_workspace_size(b, hkv, g, d, nb_max, k_cap, int(block_size))
     # the launch keeps per-row counts in its workspace from call to call: one
     # zero-filled buffer per call shape
-    ws = _scratch(workspace if workspace is not None else {}, ("topk_decode_scratch", b, hkv, g, d, nb_max, k_cap),
-                  ws_bytes, dev)
+    ws = _scratch(workspace if workspace is not None else {},
+                  ("topk_decode_scratch", b, hkv, g, d, nb_max, k_cap, int(block_size)), ws_bytes, dev)
     rc = lib.ia_sparse_topk_decode(
         sh, q.data_ptr(), kv, seq_lens.data_ptr(), keys, int(block_size), nb_max, int(k),
         None if k_per_seq is None else k_per_seq.data_ptr(), int(forced_first), int(forced_last),

@@ -84,3 +84,4 @@ def test_invalid_arguments_are_rejected_without_launching():
     rc = lib.ia_build_block_summaries(kv, None, 1, 8, 128, 64, 4, None, 1, None, 1, None, None, 1, None, None, None,
                                       None)
     assert rc == N.IA_ERR_INVALID
+

@@ -358,6 +358,30 @@ IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, co
                                  size_t workspace_bytes, void* stream);
 
 /*
+ * ia_sparse_topk_decode on a scratch buffer the library holds (no workspace
+ * argument): no counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * allocation): the call allocates nothing (no hipMalloc, hipFree or allocating
+ * library routine).  The buffer is a static device array of
+ * IA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call whose
+ * ia_sparse_topk_decode workspace would exceed it fails with IA_ERR_WORKSPACE.
+ * Every call on a GPU shares that GPU's buffer, which keeps state from call to
+ * call: when the call shape (batch, heads, head_dim, nb_max, k_cap, block_size)
+ * differs from the previous call's on that device, a clear kernel runs first on
+ * `stream` (also inside a graph being captured, where it becomes a node of the
+ * graph).  Calls that overlap on one GPU race, and so does replaying a captured
+ * graph holding this call between calls of another shape.  Results equal
+ * ia_sparse_topk_decode's, bit for bit.
+ */
+#define IA_NOALLOC_SCRATCH_BYTES (16u << 20)
+IA_API int ia_sparse_topk_decode_noalloc(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv,
+                                         const int32_t* seq_lens, const ia_block_keys* keys, int32_t block_size,
+                                         int32_t nb_max, int32_t k, const int32_t* k_per_seq,
+                                         int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
+                                         int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx,
+                                         int32_t* n_sel, void* stream);
+
+/*
  * Bound of every wait of one workgroup on another inside ia_sparse_topk_decode, in
  * ticks of the GPU's 100 MHz constant clock (default 2,000,000 = 20 ms; a negative
  * value restores it).  Returns the previous bound.  Applies to calls issued after

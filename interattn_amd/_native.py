@@ -17,6 +17,8 @@ IA_FP8_E4M3 = 2
 IA_SCORE_MEAN_KEY = 0
 IA_SCORE_QUEST = 1
 
+IA_NOALLOC_SCRATCH_BYTES = 16 << 20  # library-held scratch of ia_sparse_topk_decode_noalloc
+
 IA_OK = 0
 IA_ERR_INVALID = 1
 IA_ERR_UNSUPPORTED = 2
@@ -139,6 +141,11 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, ctypes.POINTER(BlockKeys), _I32, _I32, _I32,
          _P, _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P, _SZ, _P],
+    ),
+    "ia_sparse_topk_decode_noalloc": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(PagedKV), _P, ctypes.POINTER(BlockKeys), _I32, _I32, _I32,
+         _P, _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P],
     ),
     "ia_set_wait_limit": (_I64, [_I64]),
     "ia_select_topk_workspace_size": (_SZ, [_I32, _I32, _I32]),

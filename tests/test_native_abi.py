@@ -85,3 +85,25 @@ def test_invalid_arguments_are_rejected_without_launching():
                                       None)
     assert rc == N.IA_ERR_INVALID
 
+
+def test_noalloc_scratch_bound_matches_the_header():
+    text = open(HEADER).read()
+    m = re.search(r"#define IA_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text)
+    assert m, "IA_NOALLOC_SCRATCH_BYTES not found"
+    assert int(m.group(1)) << int(m.group(2)) == N.IA_NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_rejects_bad_arguments_before_its_scratch():
+    lib = N.lib()
+    sh = N.DecodeShape(batch=1, n_q_heads=32, n_kv_heads=8, head_dim=128, q_batch_stride=32 * 128, q_row_stride=128,
+                       q_dtype=N.IA_BF16)
+    kv = N.PagedKV()
+    keys = N.BlockKeys(score=N.IA_SCORE_MEAN_KEY, dtype=N.IA_BF16, k_bar=256)
+    for block_size, nb_max, k_cap in ((40, 8, 4), (64, -1, 4), (64, 8, 0)):
+        rc = lib.ia_sparse_topk_decode_noalloc(sh, 256, kv, 256, keys, block_size, nb_max, 4, None, 0, 0, 0, k_cap,
+                                               1.0, 256, N.IA_BF16, None, None, None)
+        assert rc == N.IA_ERR_INVALID, lib.ia_last_error()
+    sh.n_q_heads = 30  # not a multiple of the kv heads
+    rc = lib.ia_sparse_topk_decode_noalloc(sh, 256, kv, 256, keys, 64, 8, 4, None, 0, 0, 0, 4, 1.0, 256, N.IA_BF16,
+                                           None, None, None)
+    assert rc != 0

@@ -631,6 +631,18 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     auto range_lo = [&](int i) { return (int)(((long long)i * nbs) / n_it); };
     unsigned long long* row_entries = p.sbuf + (int64_t)bh * p.nb_max;
     const int own_lo = range_lo(item), own_hi = range_lo(item + 1);
+    const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
+    const TopkForced forced(rule, nbs);
+    // the candidates' largest key and largest ~key, taken while the scores pass by
+    u32 kmx = 0u, kmn_inv = 0u;
+    auto see = [&](int j, float sc) {
+      if (!forced(j)) {
+        const u32 key = order_key(sc);
+        kmx = max(kmx, key);
+        kmn_inv = max(kmn_inv, ~key);
+      }
+    };
+    bool staged = false;  // uniform: topk_stage done with the whole row's keys
     {
       constexpr int SDPL = D / 16;  // key dims per lane (16 lanes per key row)
       float qa[SDPL], qb[SDPL];     // mean key: qa = sum_g q_g; Quest: qa = sum_g q_g+, qb = sum_g q_g-
@@ -681,8 +693,11 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         if (threadIdx.x == 0) merge_todo[0] = 0u;
         __syncthreads();
         const u32 tag = row_epoch + 1u;
-        for (int j = own_lo + threadIdx.x; j < own_hi; j += kFinThreads)
-          st_agent_u64(row_entries + j, ((unsigned long long)tag << 32) | __float_as_uint(fsc[j]));
+        for (int j = own_lo + threadIdx.x; j < own_hi; j += kFinThreads) {
+          const float sc = fsc[j];
+          st_agent_u64(row_entries + j, ((unsigned long long)tag << 32) | __float_as_uint(sc));
+          see(j, sc);
+        }
         const unsigned long long t0 = clock_100mhz();
         bool missing = false;
         for (int j = threadIdx.x; j < nbs; j += kFinThreads) {
@@ -692,31 +707,33 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
             __builtin_amdgcn_s_sleep(1);
             v = ld_agent_u64(row_entries + j);
           }
-          if ((u32)(v >> 32) == tag) fsc[j] = __uint_as_float((u32)v);
-          else missing = true;
+          if ((u32)(v >> 32) == tag) {
+            const float sc = __uint_as_float((u32)v);
+            fsc[j] = sc;
+            see(j, sc);
+          } else {
+            missing = true;
+          }
         }
         if (missing) merge_todo[0] = 1u;
+        topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
         __syncthreads();
-        if (merge_todo[0]) {  // an entry missed the bound: the other items' blocks here
+        staged = merge_todo[0] == 0u;
+        if (!staged) {  // an entry missed the bound: the other items' blocks here
           score_range(0, own_lo);
           score_range(own_hi, nbs);
         }
       }
     }
-    __syncthreads();
-    // the whole score row in LDS: the shared top-k rule
-    const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
-    const TopkForced forced(rule, nbs);
-    u32 kmx = 0u, kmn_inv = 0u;
-    for (int t = threadIdx.x; t < nbs; t += kFinThreads) {
-      if (!forced(t)) {
-        const u32 key = order_key(fsc[t]);
-        kmx = max(kmx, key);
-        kmn_inv = max(kmn_inv, ~key);
-      }
+    if (!staged) {  // one pass over the whole row in LDS
+      __syncthreads();
+      kmx = 0u;
+      kmn_inv = 0u;
+      for (int t = threadIdx.x; t < nbs; t += kFinThreads) see(t, fsc[t]);
+      topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
+      __syncthreads();
     }
-    topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
-    __syncthreads();
+    // the whole score row in LDS: the shared top-k rule
     const int n_chosen = topk_select<kFinThreads, true>(
         ftk, [&](int j) -> u32 { return order_key(fsc[j]); }, nbs, rule, [&](int pos, int j) { fsel[pos] = j; });
     if (item == 0 && p.idx_out) {

@@ -162,6 +162,42 @@ __device__ __forceinline__ void threshold_bin(TopkLds<NT>& L, int remaining) {
   }
 }
 
+// The same bin computed by every wave for itself (no barrier, no LDS round trip):
+// returns (bin, count still needed inside it, members of it) as uniform values.
+__device__ __forceinline__ void threshold_bin_wave(const u32* hist, int remaining, int& bin, int& need, int& in_bin) {
+  const int lane = threadIdx.x & 63;
+  u32 c[4];
+  u32 tot = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    c[t] = hist[255 - 4 * lane - t];
+    tot += c[t];
+  }
+  const u32 inc = (u32)wave_inclusive_scan((int)tot);
+  const u32 exc = inc - tot;
+  const bool here = exc < (u32)remaining && inc >= (u32)remaining;
+  int b = 0, nd = 0, m = 0;
+  if (here) {
+    u32 run = exc;
+    bool found = false;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (!found && run + c[t] >= (u32)remaining) {
+        found = true;
+        b = 255 - 4 * lane - t;
+        nd = remaining - (int)run;
+        m = (int)c[t];
+      }
+      run += c[t];
+    }
+  }
+  const unsigned long long hit = __ballot(here);
+  const int src = hit ? __ffsll((long long)hit) - 1 : 0;
+  bin = __builtin_amdgcn_readlane(b, src);
+  need = __builtin_amdgcn_readlane(nd, src);
+  in_bin = __builtin_amdgcn_readlane(m, src);
+}
+
 struct TopkRule {
   int forced_first, forced_last, k, forced_in_k, k_cap;
 };
@@ -273,11 +309,8 @@ __device__ __forceinline__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb,
         atomicAdd(&L.hist[bucket(key_at(j))], 1u);
       }
       __syncthreads();
-      if (wave == 0) threshold_bin<NT>(L, k_eff);
-      __syncthreads();
-      const int tb = L.sh_int[1];
-      const int need = L.sh_int[2];
-      const int in_bin = L.sh_int[3];
+      int tb, need, in_bin;  // every wave finds the bin itself
+      threshold_bin_wave(L.hist, k_eff, tb, need, in_bin);
       if (in_bin <= kTieCands) {
         for (int j = threadIdx.x; j < nb; j += NT) {
           if (is_forced(j)) continue;
@@ -332,6 +365,7 @@ __device__ __forceinline__ int topk_select(TopkLds<NT>& L, KeyAt key_at, int nb,
     }
 
     if (!fast) {
+      __syncthreads();  // every wave is done with the bucket histogram
       // ---- radix select on the keys: the bytes every candidate shares are skipped
       const u32 diff = kmx ^ kmn;
       const int common_bytes = diff == 0u ? 4 : (__clz((int)diff) >> 3);

@@ -67,6 +67,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of hipGraph replay")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-layout", default="split", choices=["split", "paired"],
+                    help="K/V pool layout: separate pools, or K and V of a (page, kv head) adjacent")
     ap.add_argument("--extra", default="c5,c3,c2",
                     help="other BASELINE configs timed in the same run and reported under 'extra' "
                          "(comma list; empty for none)")
@@ -80,21 +82,33 @@ def c3_lengths():
     return [int(x) for x in rng.integers(8192, 65537, size=16)]
 
 
-def make_layer(w, dev, gen, lens, table, n_pages):
+def make_layer(w, dev, gen, lens, table, n_pages, kv_layout="split"):
+    """One layer's pool, query and summaries.  kv_layout "split": separate K and V
+    pools [n_pages, Hkv, page, D]; "paired": one buffer [n_pages, Hkv, 2, page, D]
+    whose K and V of a (page, kv head) are adjacent (pool_k / pool_v are its views)."""
     hkv, page, d = w["hkv"], w["page"], w["d"]
     shape = (n_pages, hkv, page, d)
+
+    def pool_pair(dtype):
+        if kv_layout == "paired":
+            buf = torch.empty((n_pages, hkv, 2, page, d), device=dev, dtype=dtype)
+            return buf[:, :, 0], buf[:, :, 1]
+        return torch.empty(shape, device=dev, dtype=dtype), torch.empty(shape, device=dev, dtype=dtype)
+
     if w["kv"] == "fp8":
         pk = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
         pv = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
         ks = (pk.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
         vs = (pv.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
-        pool_k = (pk.float() / ks[:, :, None, None]).to(torch.float8_e4m3fn)
-        pool_v = (pv.float() / vs[:, :, None, None]).to(torch.float8_e4m3fn)
+        pool_k, pool_v = pool_pair(torch.float8_e4m3fn)
+        pool_k.copy_((pk.float() / ks[:, :, None, None]).to(torch.float8_e4m3fn))
+        pool_v.copy_((pv.float() / vs[:, :, None, None]).to(torch.float8_e4m3fn))
         del pk, pv
         scales = (ks, vs)
     else:
-        pool_k = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
-        pool_v = torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
+        pool_k, pool_v = pool_pair(torch.bfloat16)
+        pool_k.copy_(torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen))
+        pool_v.copy_(torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen))
         scales = None
     if w.get("k_outlier"):
         # C2: keys scaled per (kv head, channel) by exp(N(0,1)) ("RoPE'd keys")
@@ -264,7 +278,7 @@ def run_topk(name, args, dev, with_dense, with_cpu):
         kvec = torch.tensor(ks, device=dev, dtype=torch.int32)
         k_cap = max(ks) + w["ff"] + w["fl"]
     t_setup = time.perf_counter()
-    layers = [make_layer(w, dev, gen, lens, table, n_pages) for _ in range(args.layers)]
+    layers = [make_layer(w, dev, gen, lens, table, n_pages, args.kv_layout) for _ in range(args.layers)]
     torch.cuda.synchronize()
     print(f"[bench] workload={name} layers={args.layers} setup {time.perf_counter() - t_setup:.1f}s",
           file=sys.stderr, flush=True)

@@ -299,10 +299,13 @@ __device__ __forceinline__ int plan_row_units(const DecodeParams& p, int r) {
 // s = sum_g sum_d max(q_gd k_max_d, q_gd k_min_d) / G = (q+ . k_max + q- . k_min) / G
 // with q+ = sum_g max(q_g, 0), q- = sum_g min(q_g, 0) (qa, qb).  The arithmetic is
 // the standalone selector's (block_score / block_score_quest), so both give the same
-// bits.  Scores land in s_lds[j].
-template <int D, bool KBF16, bool QUEST>
-__device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_off, int lo, int hi, const float* qa,
-                                             const float* qb, float* s_lds) {
+// bits.  Scores land in s_lds[j].  qw holds the raw query words of the group's rows
+// at this lane's dims (f32 q: floats; bf16 q: pairs in the first D/32 words); they
+// are summed after the first step batch's loads are issued, so the caller's query
+// loads share that round trip.
+template <int D, int G, bool KBF16, bool QUEST>
+__device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_off, int lo, int hi,
+                                             const u32 (&qw)[G][D / 16], float* s_lds) {
   constexpr int DPL = D / 16;
   constexpr int EB = KBF16 ? 2 : 4;
   constexpr int NWR = DPL * EB / 4;                  // words per lane per key row
@@ -315,10 +318,9 @@ __device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_o
   const int r = lane >> 4;
   const char* k1 = reinterpret_cast<const char*>(p.kb) + kb_off * EB;
   const char* k2 = reinterpret_cast<const char*>(p.kb2) + kb_off * EB;
-  for (int base = lo; base < hi; base += 32 * NS) {
-    words_t w;
-    // the loads of every step that holds a block of the range are issued without a
-    // per-lane condition (rows past hi re-read row hi - 1); steps past it are skipped
+  // the loads of every step that holds a block of the range are issued without a
+  // per-lane condition (rows past hi re-read row hi - 1); steps past it are skipped
+  auto issue = [&](int base, words_t& w) {
 #pragma unroll
     for (int t = 0; t < NS; ++t) {
       if (base + 32 * t >= hi) break;  // uniform
@@ -343,6 +345,8 @@ __device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_o
         }
       }
     }
+  };
+  auto compute = [&](int base, const words_t& w, const float* qa, const float* qb) {
 #pragma unroll
     for (int t = 0; t < NS; ++t) {
       if (base + 32 * t >= hi) break;  // uniform
@@ -357,6 +361,35 @@ __device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_o
                             : block_score<DPL, KBF16>(w1, qa, p.score_scale);
       if (c16 == 0 && j < hi) s_lds[j] = a;
     }
+  };
+  if (lo >= hi) return;
+  words_t w;
+  issue(lo, w);
+  // qa = sum_g q_g (mean key); Quest: qa = sum_g q_g+, qb = sum_g q_g- (the standalone
+  // selector's order), while the first batch is in flight
+  float qa[DPL], qb[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) {
+    qa[e] = 0.f;
+    qb[e] = 0.f;
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) {
+      const float v = p.q_f32 ? __uint_as_float(qw[g][e]) : ((e & 1) ? bf16_hi(qw[g][e >> 1]) : bf16_lo(qw[g][e >> 1]));
+      if constexpr (QUEST) {
+        qa[e] += fmaxf(v, 0.f);
+        qb[e] += fminf(v, 0.f);
+      } else {
+        qa[e] += v;
+      }
+    }
+  }
+  compute(lo, w, qa, qb);
+  for (int base = lo + 32 * NS; base < hi; base += 32 * NS) {
+    issue(base, w);
+    compute(base, w, qa, qb);
   }
 }
 
@@ -575,16 +608,58 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     PlanEntry e;
     if constexpr (SRC == kSrcTopkFused) {
       // every wave evaluates the launch plan itself (no barrier, no round trip to a
-      // plan written elsewhere): a row's units are the blocks the top-k rule takes
+      // plan written elsewhere): a row's units are the blocks the top-k rule takes.
+      // The lengths and k of the rows a lane holds in registers are loaded first, all
+      // in one round trip (clamped indices, no per-lane branch).
+      int pre_len[kPlanRegRows], pre_k[kPlanRegRows];
+      const int last_row = max(p.n_rows - 1, 0);
+#pragma unroll
+      for (int k = 0; k < kPlanRegRows; ++k) pre_len[k] = p.seq_lens[min(lane + 64 * k, last_row) / p.n_kv_heads];
+      if (p.k_per_seq) {
+#pragma unroll
+        for (int k = 0; k < kPlanRegRows; ++k) pre_k[k] = p.k_per_seq[min(lane + 64 * k, last_row) / p.n_kv_heads];
+      } else {
+#pragma unroll
+        for (int k = 0; k < kPlanRegRows; ++k) pre_k[k] = p.topk_k;
+      }
+      auto row_slots = [&](int len, int kr) -> int {
+        const int nbs_r = min(cdiv_pos(max(len, 0), p.unit_tokens), p.nb_max);
+        return topk_count(nbs_r, TopkRule{p.forced_first, p.forced_last, max(kr, 0), p.forced_in_k, p.k_cap}) *
+               nsub_u;
+      };
       auto slots_of = [&](int rr) -> int {
+        if ((rr & 63) == lane && (rr >> 6) < kPlanRegRows) {
+          int len = pre_len[0], kr = pre_k[0];
+#pragma unroll
+          for (int k = 1; k < kPlanRegRows; ++k)
+            if ((rr >> 6) == k) {
+              len = pre_len[k];
+              kr = pre_k[k];
+            }
+          return row_slots(len, kr);
+        }
         const int bb = rr / p.n_kv_heads;
-        const int kr = p.k_per_seq ? max(p.k_per_seq[bb], 0) : p.topk_k;
-        const int nbs_r = min(cdiv_pos(max(p.seq_lens[bb], 0), p.unit_tokens), p.nb_max);
-        return topk_count(nbs_r, TopkRule{p.forced_first, p.forced_last, kr, p.forced_in_k, p.k_cap}) * nsub_u;
+        return row_slots(p.seq_lens[bb], p.k_per_seq ? p.k_per_seq[bb] : p.topk_k);
       };
       PlanRows rows;
       const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
       e = plan_entry_wave(slots_of, rows, p.n_rows, rule, (int)blockIdx.x, nsub_u);
+      // the row's length and k from the lane that holds it
+      const int row_e = __builtin_amdgcn_readfirstlane(e.row);
+      if (row_e >= 0 && row_e < 64 * kPlanRegRows) {
+        int len = pre_len[0], kr = pre_k[0];
+#pragma unroll
+        for (int k = 1; k < kPlanRegRows; ++k)
+          if ((row_e >> 6) == k) {
+            len = pre_len[k];
+            kr = pre_k[k];
+          }
+        e.seq_len = __builtin_amdgcn_readlane(len, row_e & 63);
+        e.k_row = __builtin_amdgcn_readlane(kr, row_e & 63);
+      } else if (row_e >= 0) {
+        e.seq_len = p.seq_lens[row_e / p.n_kv_heads];
+        e.k_row = p.k_per_seq ? p.k_per_seq[row_e / p.n_kv_heads] : p.topk_k;
+      }
     } else {
       if (wave == 0) {
         PlanRows rows;
@@ -605,17 +680,23 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     slot_lo = __builtin_amdgcn_readfirstlane(e.slot_lo);
     slot_hi = __builtin_amdgcn_readfirstlane(e.slot_hi);
     n_units = __builtin_amdgcn_readfirstlane(e.n_units);
-    seq_len = max(p.seq_lens[b], 0);
-    if constexpr (SRC == kSrcTopkFused) k_b = p.k_per_seq ? max(p.k_per_seq[b], 0) : p.topk_k;
+    if constexpr (SRC == kSrcTopkFused) {
+      seq_len = max(__builtin_amdgcn_readfirstlane(e.seq_len), 0);
+      k_b = max(__builtin_amdgcn_readfirstlane(e.k_row), 0);
+    } else {
+      seq_len = max(p.seq_lens[b], 0);
+    }
   } else {
     b = blockIdx.z;
     h = blockIdx.y;
     item = blockIdx.x;
   }
   const int bh = b * p.n_kv_heads + h;
-  if constexpr (SRC == kSrcTopkFused)
-    if (n_items_row > 1) row_epoch = __builtin_amdgcn_readfirstlane(ld_agent_u32(p.rowctr + (int64_t)bh * kFlagStride + 1));
-  load_q(b, h);
+  // (the epoch stays in a vector register until the publish, so its load is not
+  // waited for here)
+  u32 row_epoch_v = 0u;
+  if constexpr (SRC == kSrcTopkFused) row_epoch_v = ld_agent_u32(p.rowctr + (int64_t)bh * kFlagStride + 1);
+  if constexpr (SRC != kSrcTopkFused) load_q(b, h);
 
   if constexpr (SRC == kSrcTopkFused) {
     // ---- block scores: item i of the row's n scores blocks [i nbs / n, (i+1) nbs / n)
@@ -645,53 +726,35 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     bool staged = false;  // uniform: topk_stage done with the whole row's keys
     {
       constexpr int SDPL = D / 16;  // key dims per lane (16 lanes per key row)
-      float qa[SDPL], qb[SDPL];     // mean key: qa = sum_g q_g; Quest: qa = sum_g q_g+, qb = sum_g q_g-
-#pragma unroll
-      for (int e = 0; e < SDPL; ++e) {
-        qa[e] = 0.f;
-        qb[e] = 0.f;
-      }
+      // the group's query rows at this lane's dims: loads issued now, summed inside the
+      // scorer once its first key batch is in flight (one round trip for both)
+      // (the same two loads on both q dtypes, no branch: f32 rows read their two
+      // halves, bf16 rows their one slice twice)
+      u32 qw[G][SDPL];
+      const int q_es = p.q_f32 ? 4 : 2;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int64_t qrow = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * SDPL;
-        float v[SDPL];
-        if (p.q_f32) {
-#pragma unroll
-          for (int e = 0; e < SDPL; ++e) v[e] = reinterpret_cast<const float*>(p.q)[qrow + e];
-        } else {
-          u32 w[SDPL / 2];
-          load_words<SDPL / 2>(reinterpret_cast<const char*>(reinterpret_cast<const unsigned short*>(p.q) + qrow), w);
-#pragma unroll
-          for (int e = 0; e < SDPL / 2; ++e) {
-            v[2 * e] = bf16_lo(w[e]);
-            v[2 * e + 1] = bf16_hi(w[e]);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < SDPL; ++e) {
-          if (p.score_quest) {
-            qa[e] += fmaxf(v[e], 0.f);
-            qb[e] += fminf(v[e], 0.f);
-          } else {
-            qa[e] += v[e];  // same order as the standalone selector's sum
-          }
-        }
+        const char* q0 = reinterpret_cast<const char*>(p.q) + qrow * q_es;
+        load_words<SDPL / 2>(q0, qw[g]);
+        load_words<SDPL / 2>(p.q_f32 ? q0 + SDPL * 2 : q0, qw[g] + SDPL / 2);
       }
       const int64_t kb_off = (int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride;
       // blocks [lo, hi): 32 per workgroup step (wave w, lane row r: block 32 t + 4 w + r)
       auto score_range = [&](int lo, int hi) {
         if (p.score_quest) {
-          if (p.kb_bf16) score_blocks<D, true, true>(p, kb_off, lo, hi, qa, qb, fsc);
-          else score_blocks<D, false, true>(p, kb_off, lo, hi, qa, qb, fsc);
+          if (p.kb_bf16) score_blocks<D, G, true, true>(p, kb_off, lo, hi, qw, fsc);
+          else score_blocks<D, G, false, true>(p, kb_off, lo, hi, qw, fsc);
         } else {
-          if (p.kb_bf16) score_blocks<D, true, false>(p, kb_off, lo, hi, qa, qb, fsc);
-          else score_blocks<D, false, false>(p, kb_off, lo, hi, qa, qb, fsc);
+          if (p.kb_bf16) score_blocks<D, G, true, false>(p, kb_off, lo, hi, qw, fsc);
+          else score_blocks<D, G, false, false>(p, kb_off, lo, hi, qw, fsc);
         }
       };
       score_range(own_lo, own_hi);
       if (n_it > 1) {
         if (threadIdx.x == 0) merge_todo[0] = 0u;
         __syncthreads();
+        row_epoch = __builtin_amdgcn_readfirstlane(row_epoch_v);
         const u32 tag = row_epoch + 1u;
         for (int j = own_lo + threadIdx.x; j < own_hi; j += kFinThreads) {
           const float sc = fsc[j];
@@ -716,6 +779,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
           }
         }
         if (missing) merge_todo[0] = 1u;
+        load_q(b, h);  // the stream's query operands: in flight during the selection
         topk_stage<kFinThreads>(ftk, kmx, kmn_inv);
         __syncthreads();
         staged = merge_todo[0] == 0u;
@@ -726,6 +790,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     }
     if (!staged) {  // one pass over the whole row in LDS
+      if (n_it == 1) load_q(b, h);
       __syncthreads();
       kmx = 0u;
       kmn_inv = 0u;

@@ -8,7 +8,8 @@ merges).  The default workload is
 batch 16, 131072-token contexts, 32 query / 8 KV heads, head_dim
 128, KV block 128, top-64 blocks per KV head, bf16 K/V in a paged pool of 16-token
 pages in randomly permuted order, bf16 k_bar summaries.  Inputs are synthetic
-(q, K, V ~ N(0,1)), resident in HBM before timing starts.  ``--layers`` independent
+(q, K, V ~ N(0,1)), resident in HBM before timing starts; by default K and V of a
+(page, kv head) sit next to each other in one buffer (``--kv-layout``).  ``--layers`` independent
 pools are rotated through so consecutive calls never re-read the same K/V pages
 (the 256 MB MALL cannot hold the per-call working set).
 
@@ -67,8 +68,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of hipGraph replay")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kv-layout", default="split", choices=["split", "paired"],
-                    help="K/V pool layout: separate pools, or K and V of a (page, kv head) adjacent")
+    ap.add_argument("--kv-layout", default="paired", choices=["split", "paired"],
+                    help="K/V pool layout: K and V of a (page, kv head) adjacent in one buffer (paired: "
+                         "one 8 KiB run per bf16 page and head), or separate K and V pools (split)")
     ap.add_argument("--extra", default="c5,c3,c2",
                     help="other BASELINE configs timed in the same run and reported under 'extra' "
                          "(comma list; empty for none)")
@@ -402,6 +404,7 @@ def run_topk(name, args, dev, with_dense, with_cpu):
     torch.cuda.empty_cache()
     gbps = total_bytes / (us_per_layer * 1e-6) / 1e9
     return dict(w=w, lens=lens, steps=steps, us=us_per_layer, timing=tim, wall=wall, use_graph=use_graph, nl=nl,
+                kv_layout=args.kv_layout,
                 total_bytes=total_bytes, qo_b=qo_b, summ_b=summ_b, kv_b=kv_b, gbps=gbps, call_us=call_us,
                 sel_us=sel_us, fin_us=fin_us, fin_bytes=fin_bytes, dense_us=dense_us, dense_bytes=dense_bytes,
                 cpu=cpu)
@@ -426,7 +429,7 @@ def config_of(name, r):
             "page": w["page"], "top_k": w["k"] if w["k"] else "max(16, nb/16)",
             "forced_first": w["ff"], "forced_last": w["fl"], "kv_dtype": w["kv"],
             "k_outlier": bool(w.get("k_outlier")), "layers_rotated": r["nl"],
-            "launch": "hipgraph" if r["use_graph"] else "eager"}
+            "launch": "hipgraph" if r["use_graph"] else "eager", "kv_layout": r["kv_layout"]}
 
 
 def main():

@@ -216,7 +216,8 @@ FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap,
   L.part_ml = align_up(L.sbuf + (size_t)rows * std::max(nb_max, 1) * 8, 256);
   L.part_acc = align_up(L.part_ml + (size_t)L.slots * g * 2 * 4, 256);
   L.part_n = align_up(L.part_acc + (size_t)L.slots * g * d * 4, 256);
-  L.total = align_up(L.part_n + (size_t)rows * 4, 256);
+  L.tpart = align_up(L.part_n + (size_t)rows * 4, 256);
+  L.total = align_up(L.tpart + (size_t)L.slots * (g * d + 2 * g) * 8, 256);
   return L;
 }
 
@@ -297,6 +298,7 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   p.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
   p.part_acc = reinterpret_cast<float*>(ws + L.part_acc);
   p.part_n = reinterpret_cast<int32_t*>(ws + L.part_n);
+  p.tpart = reinterpret_cast<unsigned long long*>(ws + L.tpart);
   return dispatch_decode(p, kv->dtype, D, G, kSrcTopkFused, dim3(grid), st, nullptr);
 }
 

@@ -154,6 +154,7 @@ struct DecodeParams {
   int32_t score_quest;
   float score_scale;
   unsigned long long* sbuf;  // [rows, nb_max] published scores: tag << 32 | score bits
+  unsigned long long* tpart; // [workgroups, G D + 2 G] tagged partials (acc, then (m, l)) of rows of <= 8 items
   u32* rowctr;               // [rows, kFlagStride]: finished partials (word 0), row epoch (word 1)
   int64_t wait_ticks;
 };
@@ -525,6 +526,69 @@ __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h,
     }
     merge_combine<1>(
         ng, [&](int g) { return gM[g]; }, [&](int g) { return gL[g]; }, [&](int g, int) { return ga[g][0]; },
+        [&](int, float v) { store_decode_out<G, D>(p, b, h, o, v); });
+  }
+}
+
+// A workgroup's split-K slot serves whichever row the launch plan gives it, so the
+// tag of a tagged partial names the row too: row << 19 | (epoch + 1) mod 2^19 (rows
+// < 2^13).  A slot's earlier contents then never match unless they are 2^19 calls
+// of the same row old.
+__device__ __forceinline__ u32 partial_tag(int bh, u32 row_epoch) {
+  return ((u32)bh << 19) | ((row_epoch + 1u) & 0x7ffffu);
+}
+
+// The merge of a row of at most kMergeGroup items whose partials were published as
+// tagged 8-byte words (value bits | tag << 32, tag = partial_tag): every
+// slot's words are loaded at once and a word whose tag has not arrived yet is read
+// again (its publisher has passed the row's counter, so its stores are in flight).
+// One merge group: the merge kernel's arithmetic, the same bits.  A word still
+// missing at the wait bound turns the output into NaN (never silent).
+template <int D, int G>
+__device__ __forceinline__ void fused_merge_tagged(const DecodeParams& p, int b, int h, int64_t slot0, int n, u32 tag) {
+  constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
+  constexpr int W = G * D + 2 * G;                             // words per slot
+  __shared__ float mlt_lds[kMergeGroup][G][2];
+  const unsigned long long t0 = clock_100mhz();
+  auto value = [&](const unsigned long long* ptr, unsigned long long v) -> float {
+    while ((u32)(v >> 32) != tag && (long long)(clock_100mhz() - t0) <= p.wait_ticks) {
+      __builtin_amdgcn_s_sleep(1);
+      v = ld_agent_u64(ptr);
+    }
+    return (u32)(v >> 32) == tag ? __uint_as_float((u32)v) : __builtin_nanf("");
+  };
+  // (m, l) of every slot, staged in LDS
+  if (threadIdx.x < kMergeGroup * G * 2) {
+    const int s = threadIdx.x / (G * 2), e = threadIdx.x % (G * 2);
+    const unsigned long long* ptr = p.tpart + (slot0 + min(s, n - 1)) * W + G * D + e;
+    const float v = value(ptr, ld_agent_u64(ptr));
+    if (s < n) mlt_lds[s][e / 2][e % 2] = v;
+  }
+#pragma unroll 1
+  for (int k = 0; k < NO; ++k) {
+    const int o = threadIdx.x + kFinThreads * k;
+    unsigned long long raw[kMergeGroup];
+    const bool active = o < G * D;
+    const int oc = active ? o : 0;
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j) raw[j] = ld_agent_u64(p.tpart + (slot0 + min(j, n - 1)) * W + oc);
+    float av[kMergeGroup][1];
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j)
+      av[j][0] = j < n ? value(p.tpart + (slot0 + j) * W + oc, raw[j]) : 0.f;
+    if (k == 0) __syncthreads();  // the (m, l) staging
+    if (!active) continue;
+    const int g0 = o / D;
+    float mv[kMergeGroup], lv[kMergeGroup];
+#pragma unroll
+    for (int j = 0; j < kMergeGroup; ++j) {
+      mv[j] = j < n ? mlt_lds[j][g0][0] : kNegInf;
+      lv[j] = j < n ? mlt_lds[j][g0][1] : 0.f;
+    }
+    float gM, gL, ga[1];
+    merge_group<1>(mv, lv, av, gM, gL, ga);
+    merge_combine<1>(
+        1, [&](int) { return gM; }, [&](int) { return gL; }, [&](int, int) { return ga[0]; },
         [&](int, float v) { store_decode_out<G, D>(p, b, h, o, v); });
   }
 }
@@ -1462,6 +1526,15 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
     if (!split) {
       store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
+    } else if (SRC == kSrcTopkFused && n_items_row <= kMergeGroup) {
+      // tagged words: readable as soon as they land, no acknowledgement to wait for
+      const unsigned long long tg = (unsigned long long)partial_tag(bh, row_epoch) << 32;
+      unsigned long long* slot = p.tpart + pbase * (G * D + 2 * G);
+      st_agent_u64(slot + o, tg | __float_as_uint(a));
+      if (o % D == 0) {
+        st_agent_u64(slot + G * D + 2 * g, tg | __float_as_uint(M));
+        st_agent_u64(slot + G * D + 2 * g + 1, tg | __float_as_uint(l));
+      }
     } else if (SRC == kSrcTopkFused) {
       st_agent(p.part_acc + pbase * (G * D) + o, a);
       if (o % D == 0) {
@@ -1479,10 +1552,11 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   if constexpr (SRC == kSrcTopkFused) {
     if (split) {
       // the row's items count their finished partials; the one that brings the count
-      // to n merges (every partial is then at the coherence point) and resets the
-      // count for the next call: nobody waits, so nothing depends on which
-      // workgroups are resident together
-      wait_memory();
+      // to n merges and resets the count for the next call.  Untagged partials (rows
+      // of more than kMergeGroup items) are at the coherence point before the count
+      // moves; tagged ones are read again until their tag arrives.  No item waits
+      // for another's work, so nothing depends on which workgroups run together.
+      if (n_items_row > kMergeGroup) wait_memory();
       __syncthreads();
       if (threadIdx.x == 0) {
         u32* ctr = p.rowctr + (int64_t)bh * kFlagStride;
@@ -1495,7 +1569,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         merge_todo[0] = last ? 1u : 0u;
       }
       __syncthreads();
-      if (merge_todo[0]) fused_merge<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row);
+      if (merge_todo[0]) {
+        if (n_items_row <= kMergeGroup)
+          fused_merge_tagged<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row, partial_tag(bh, row_epoch));
+        else
+          fused_merge<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row);
+      }
     }
   }
 }
@@ -1827,7 +1906,7 @@ int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int
 // per workgroup ((m, l) [slot, G, 2], acc [slot, G, D]) and the items per row.
 // The part before part_ml carries state from call to call (zero-filled at first).
 struct FusedWs {
-  size_t sbuf, part_ml, part_acc, part_n, total;
+  size_t sbuf, part_ml, part_acc, part_n, tpart, total;
   int64_t slots;
 };
 FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size);

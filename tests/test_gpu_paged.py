@@ -528,3 +528,38 @@ def test_fused_handoff_fallback_is_exact(name, device):
     torch.cuda.synchronize()
     for r, a, b_ in zip(refs, got0, got):
         assert torch.equal(a, r) and torch.equal(b_, r)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("c", [CASES[7], CASES[2]], ids=[CASES[7][0], CASES[2][0]])
+def test_paired_kv_layout_equals_split(c, fp8, device):
+    """K and V of a (page, kv head) adjacent in one buffer [n_pages, Hkv, 2, page, D]
+    (pool_k / pool_v are its views, bench.py --kv-layout paired): the one-launch call
+    and the summaries equal those of separate pools bit for bit."""
+    name, b, hq, hkv, d, lens, page, block, dt, sel, _ = c
+    k, ff, fl, in_k = sel
+    announce(f"paired kv layout {name} fp8={fp8}")
+    case = _build(c, fp8=fp8)
+    dev = to_dev(case, device, _torch_dtype(dt), fp8=fp8)
+    buf = torch.empty((dev["pool_k"].shape[0], hkv, 2, page, d), device=device, dtype=dev["pool_k"].dtype)
+    buf[:, :, 0].copy_(dev["pool_k"])
+    buf[:, :, 1].copy_(dev["pool_v"])
+    pk, pv = buf[:, :, 0], buf[:, :, 1]
+    nb_max = max(math.ceil(L / block) for L in lens)
+    kw = dict(block_size=block, forced_first=ff, forced_last=fl, forced_in_k=in_k)
+    outs = []
+    for pool_k, pool_v in ((dev["pool_k"], dev["pool_v"]), (pk, pv)):
+        summ = ia.build_block_summaries(pool_k, pool_v, dev["block_table"], dev["seq_lens"], block, nb_max=nb_max,
+                                        k_bar_dtype=torch.bfloat16, scales=dev["scales"])
+        out, idx, n_sel = ia.sparse_topk_decode(dev["q"], pool_k, pool_v, dev["block_table"], dev["seq_lens"],
+                                                summ["k_bar"], k, scales=dev["scales"], return_selection=True,
+                                                workspace={}, **kw)
+        outs.append((summ["k_bar"].clone(), out.clone(), idx.clone(), n_sel.clone()))
+    torch.cuda.synchronize()
+    (kb0, o0, i0, n0), (kb1, o1, i1, n1) = outs
+    assert torch.equal(kb0, kb1)
+    assert torch.equal(n0, n1) and torch.equal(o0, o1)
+    for i in range(b):
+        for h in range(hkv):
+            n = int(n0[i, h])
+            assert torch.equal(i0[i, h, :n], i1[i, h, :n])

@@ -68,7 +68,7 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead of hipGraph replay")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--kv-layout", default="paired", choices=["split", "paired"],
+    ap.add_argument("--kv-layout", default="paired", choices=["split", "paired", "head_paired"],
                     help="K/V pool layout: K and V of a (page, kv head) adjacent in one buffer (paired: "
                          "one 8 KiB run per bf16 page and head), or separate K and V pools (split)")
     ap.add_argument("--extra", default="c5,c3,c2",
@@ -95,6 +95,9 @@ def make_layer(w, dev, gen, lens, table, n_pages, kv_layout="split"):
         if kv_layout == "paired":
             buf = torch.empty((n_pages, hkv, 2, page, d), device=dev, dtype=dtype)
             return buf[:, :, 0], buf[:, :, 1]
+        if kv_layout == "head_paired":
+            buf = torch.empty((hkv, n_pages, 2, page, d), device=dev, dtype=dtype)
+            return buf[:, :, 0].transpose(0, 1), buf[:, :, 1].transpose(0, 1)
         return torch.empty(shape, device=dev, dtype=dtype), torch.empty(shape, device=dev, dtype=dtype)
 
     if w["kv"] == "fp8":

@@ -303,25 +303,31 @@ __device__ __forceinline__ int plan_row_units(const DecodeParams& p, int r) {
 // bits.  Scores land in s_lds[j].  qw holds the raw query words of the group's rows
 // at this lane's dims (f32 q: floats; bf16 q: pairs in the first D/32 words); they
 // are summed after the first step batch's loads are issued, so the caller's query
-// loads share that round trip.
-template <int D, int G, bool KBF16, bool QUEST>
-__device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_off, int lo, int hi,
-                                             const u32 (&qw)[G][D / 16], float* s_lds) {
-  constexpr int DPL = D / 16;
-  constexpr int EB = KBF16 ? 2 : 4;
-  constexpr int NWR = DPL * EB / 4;                  // words per lane per key row
-  constexpr int NW = D >= 128 ? 64 : 32;             // key words per lane in flight
-  constexpr int NS = NW / NWR / (QUEST ? 2 : 1);     // steps in flight (Quest reads two rows per block)
-  typedef u32 __attribute__((ext_vector_type(NW))) words_t;  // a value: registers, never memory
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c16 = lane & 15;
-  const int r = lane >> 4;
-  const char* k1 = reinterpret_cast<const char*>(p.kb) + kb_off * EB;
-  const char* k2 = reinterpret_cast<const char*>(p.kb2) + kb_off * EB;
-  // the loads of every step that holds a block of the range are issued without a
-  // per-lane condition (rows past hi re-read row hi - 1); steps past it are skipped
-  auto issue = [&](int base, words_t& w) {
+// loads share that round trip.  SHARED: the rows are read by other workgroups of the
+// same XCD too (plain loads, so their lines stay in L2 for them); else streaming loads.
+// key words per lane in flight in one step batch of the scorer (a value: registers,
+// never memory)
+template <int D>
+using ScoreWords = u32 __attribute__((ext_vector_type(D >= 128 ? 64 : 32)));
+
+template <int D, int G, bool KBF16, bool QUEST, bool SHARED>
+struct BlockScorer {
+  static constexpr int DPL = D / 16;
+  static constexpr int EB = KBF16 ? 2 : 4;
+  static constexpr int NWR = DPL * EB / 4;                        // words per lane per key row
+  static constexpr int NW = D >= 128 ? 64 : 32;                   // key words per lane in flight
+  static constexpr int NS = NW / NWR / (QUEST ? 2 : 1);           // steps in flight (Quest reads two rows per block)
+  using words_t = ScoreWords<D>;
+
+  // the loads of every step of the batch at base that holds a block of [.., hi), without
+  // a per-lane condition (rows past hi re-read row hi - 1); steps past it are skipped
+  __device__ __forceinline__ static void issue(const DecodeParams& p, int64_t kb_off, int base, int hi, words_t& w) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c16 = lane & 15;
+    const int r = lane >> 4;
+    const char* k1 = reinterpret_cast<const char*>(p.kb) + kb_off * EB;
+    const char* k2 = reinterpret_cast<const char*>(p.kb2) + kb_off * EB;
 #pragma unroll
     for (int t = 0; t < NS; ++t) {
       if (base + 32 * t >= hi) break;  // uniform
@@ -333,65 +339,80 @@ __device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_o
         if constexpr (NWR >= 4) {
 #pragma unroll
           for (int v4 = 0; v4 < NWR; v4 += 4) {
-            const u32x4_t x = ld_stream16(rowp + 4 * v4);
+            const u32x4_t x = SHARED ? *reinterpret_cast<const u32x4_t*>(rowp + 4 * v4) : ld_stream16(rowp + 4 * v4);
             w[o + v4] = x[0];
             w[o + v4 + 1] = x[1];
             w[o + v4 + 2] = x[2];
             w[o + v4 + 3] = x[3];
           }
         } else {
-          const u32x2_t x = ld_stream8(rowp);
+          const u32x2_t x = SHARED ? *reinterpret_cast<const u32x2_t*>(rowp) : ld_stream8(rowp);
           w[o] = x[0];
           w[o + 1] = x[1];
         }
       }
     }
-  };
-  auto compute = [&](int base, const words_t& w, const float* qa, const float* qb) {
-#pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      if (base + 32 * t >= hi) break;  // uniform
-      const int j = base + 32 * t + 4 * wave + r;
-      u32 w1[NWR], w2[NWR];
-#pragma unroll
-      for (int e = 0; e < NWR; ++e) {
-        w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
-        w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
-      }
-      const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qa, qb, p.score_scale)
-                            : block_score<DPL, KBF16>(w1, qa, p.score_scale);
-      if (c16 == 0 && j < hi) s_lds[j] = a;
-    }
-  };
-  if (lo >= hi) return;
-  words_t w;
-  issue(lo, w);
-  // qa = sum_g q_g (mean key); Quest: qa = sum_g q_g+, qb = sum_g q_g- (the standalone
-  // selector's order), while the first batch is in flight
-  float qa[DPL], qb[DPL];
-#pragma unroll
-  for (int e = 0; e < DPL; ++e) {
-    qa[e] = 0.f;
-    qb[e] = 0.f;
   }
+
+  // Scores of blocks [lo, hi) into s_lds
+  __device__ __forceinline__ static void run(const DecodeParams& p, int64_t kb_off, int lo, int hi,
+                                             const u32 (&qw)[G][D / 16], float* s_lds, words_t& w) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int c16 = lane & 15;
+    const int r = lane >> 4;
+    auto compute = [&](int base, const words_t& wv, const float* qa, const float* qb) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+      for (int t = 0; t < NS; ++t) {
+        if (base + 32 * t >= hi) break;  // uniform
+        const int j = base + 32 * t + 4 * wave + r;
+        u32 w1[NWR], w2[NWR];
+#pragma unroll
+        for (int e = 0; e < NWR; ++e) {
+          w1[e] = wv[(QUEST ? 2 * t : t) * NWR + e];
+          w2[e] = QUEST ? wv[(2 * t + 1) * NWR + e] : 0u;
+        }
+        const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qa, qb, p.score_scale)
+                              : block_score<DPL, KBF16>(w1, qa, p.score_scale);
+        if (c16 == 0 && j < hi) s_lds[j] = a;
+      }
+    };
+    if (lo >= hi) return;
+    issue(p, kb_off, lo, hi, w);
+    // qa = sum_g q_g (mean key); Quest: qa = sum_g q_g+, qb = sum_g q_g- (the standalone
+    // selector's order), while the first batch is in flight
+    float qa[DPL], qb[DPL];
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
-      const float v = p.q_f32 ? __uint_as_float(qw[g][e]) : ((e & 1) ? bf16_hi(qw[g][e >> 1]) : bf16_lo(qw[g][e >> 1]));
-      if constexpr (QUEST) {
-        qa[e] += fmaxf(v, 0.f);
-        qb[e] += fminf(v, 0.f);
-      } else {
-        qa[e] += v;
+      qa[e] = 0.f;
+      qb[e] = 0.f;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const float v = p.q_f32 ? __uint_as_float(qw[g][e]) : ((e & 1) ? bf16_hi(qw[g][e >> 1]) : bf16_lo(qw[g][e >> 1]));
+        if constexpr (QUEST) {
+          qa[e] += fmaxf(v, 0.f);
+          qb[e] += fminf(v, 0.f);
+        } else {
+          qa[e] += v;
+        }
       }
     }
+    compute(lo, w, qa, qb);
+    for (int base = lo + 32 * NS; base < hi; base += 32 * NS) {
+      issue(p, kb_off, base, hi, w);
+      compute(base, w, qa, qb);
+    }
   }
-  compute(lo, w, qa, qb);
-  for (int base = lo + 32 * NS; base < hi; base += 32 * NS) {
-    issue(base, w);
-    compute(base, w, qa, qb);
-  }
+};
+
+template <int D, int G, bool KBF16, bool QUEST, bool SHARED>
+__device__ __forceinline__ void score_blocks(const DecodeParams& p, int64_t kb_off, int lo, int hi,
+                                             const u32 (&qw)[G][D / 16], float* s_lds) {
+  ScoreWords<D> w;
+  BlockScorer<D, G, KBF16, QUEST, SHARED>::run(p, kb_off, lo, hi, qw, s_lds, w);
 }
 
 constexpr int kMaxMergeSlots = kMaxItemsPerBh + kMaxRouteChunks;  // split-K items + representative partials
@@ -399,6 +420,7 @@ constexpr int kMergeFastSlots = 8;  // slots per wave read in the merge's one-ro
 constexpr int kMergeGroup = kMergeFastSlots;            // slots per merge group
 constexpr int kMergeGroups = kMaxItemsPerBh / kMergeGroup;  // groups of a row's split-K items
 constexpr int kFlagStride = 64;  // u32 words between hand-off flags (one 256-byte line each)
+constexpr int kSoloItems = 2;    // fused top-k call: rows of at most this many items score the whole row per item
 
 // The split-K merge of a row's items (balanced launches: the merge kernel and the
 // fused top-k call's in-kernel merge share it, so both give the same bits).  Slots
@@ -668,6 +690,16 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     }
   };
   u32 row_epoch = 0u;  // fused top-k call: calls so far that split this row
+  // fused top-k call: the plan slot of this workgroup.  Workgroup w runs on XCD w % 8
+  // (the dispatcher deals workgroups to the XCDs in turn), so slot
+  // (w % 8) * (grid / 8) + w / 8 puts consecutive slots -- the items of one row -- on
+  // one XCD, where they share the row's block-key lines through its L2.  (Placement
+  // only: any mapping gives the same results.)
+  bool rows_alike = false;  // fused top-k call: every row has the same work (uniform)
+  constexpr int SDPL = D / 16;  // key dims per lane in the scorer (16 lanes per key row)
+  const int fused_slot = (gridDim.x % 8 == 0)
+                             ? (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8)
+                             : (int)blockIdx.x;
   if constexpr (kBalanced) {
     PlanEntry e;
     if constexpr (SRC == kSrcTopkFused) {
@@ -707,7 +739,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       };
       PlanRows rows;
       const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
-      e = plan_entry_wave(slots_of, rows, p.n_rows, rule, (int)blockIdx.x, nsub_u);
+      rows_alike = rule.n_all > 0;
+      e = plan_entry_wave(slots_of, rows, p.n_rows, rule, fused_slot, nsub_u);
       // the row's length and k from the lane that holds it
       const int row_e = __builtin_amdgcn_readfirstlane(e.row);
       if (row_e >= 0 && row_e < 64 * kPlanRegRows) {
@@ -773,9 +806,19 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     // (item 0 publishes the chosen blocks).
     const int nbs = min(cdiv_pos(seq_len, p.unit_tokens), p.nb_max);
     const int n_it = n_items_row;
-    auto range_lo = [&](int i) { return (int)(((long long)i * nbs) / n_it); };
+    // (G > 4 keeps the hand-off: its query words leave no room for a second scorer form)
+    constexpr bool kSoloG = G <= 4;
+    // rows of up to kSoloItems items of a launch whose rows are alike: every item
+    // scores the whole row itself (the row's items sit on one XCD and read the key
+    // lines in the same order, so the second read of a line is an L2 hit) and no
+    // scores are handed over; other rows split the scoring and hand the scores to
+    // each other.  Measured (alternating builds on one box): C5 66.4 against 67.8 us,
+    // C4 unchanged; ragged C3 rows were 0.3-0.8 us slower whole-row, so they keep the
+    // hand-off.
+    const bool solo = kSoloG && n_it <= kSoloItems && rows_alike;
+    auto range_lo = [&](int i) { return (i * nbs) / n_it; };  // (< 2^19: 32-bit arithmetic)
     unsigned long long* row_entries = p.sbuf + (int64_t)bh * p.nb_max;
-    const int own_lo = range_lo(item), own_hi = range_lo(item + 1);
+    const int own_lo = solo ? 0 : range_lo(item), own_hi = solo ? nbs : range_lo(item + 1);
     const TopkRule rule{p.forced_first, p.forced_last, k_b, p.forced_in_k, p.k_cap};
     const TopkForced forced(rule, nbs);
     // the candidates' largest key and largest ~key, taken while the scores pass by
@@ -789,7 +832,6 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     };
     bool staged = false;  // uniform: topk_stage done with the whole row's keys
     {
-      constexpr int SDPL = D / 16;  // key dims per lane (16 lanes per key row)
       // the group's query rows at this lane's dims: loads issued now, summed inside the
       // scorer once its first key batch is in flight (one round trip for both)
       // (the same two loads on both q dtypes, no branch: f32 rows read their two
@@ -806,16 +848,24 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       const int64_t kb_off = (int64_t)b * p.kb_batch_stride + (int64_t)h * p.kb_head_stride;
       // blocks [lo, hi): 32 per workgroup step (wave w, lane row r: block 32 t + 4 w + r)
       auto score_range = [&](int lo, int hi) {
-        if (p.score_quest) {
-          if (p.kb_bf16) score_blocks<D, G, true, true>(p, kb_off, lo, hi, qw, fsc);
-          else score_blocks<D, G, false, true>(p, kb_off, lo, hi, qw, fsc);
+        if (kSoloG && solo && n_it > 1) {
+          if (p.score_quest) {
+            if (p.kb_bf16) score_blocks<D, G, true, true, true>(p, kb_off, lo, hi, qw, fsc);
+            else score_blocks<D, G, false, true, true>(p, kb_off, lo, hi, qw, fsc);
+          } else {
+            if (p.kb_bf16) score_blocks<D, G, true, false, true>(p, kb_off, lo, hi, qw, fsc);
+            else score_blocks<D, G, false, false, true>(p, kb_off, lo, hi, qw, fsc);
+          }
+        } else if (p.score_quest) {
+          if (p.kb_bf16) score_blocks<D, G, true, true, false>(p, kb_off, lo, hi, qw, fsc);
+          else score_blocks<D, G, false, true, false>(p, kb_off, lo, hi, qw, fsc);
         } else {
-          if (p.kb_bf16) score_blocks<D, G, true, false>(p, kb_off, lo, hi, qw, fsc);
-          else score_blocks<D, G, false, false>(p, kb_off, lo, hi, qw, fsc);
+          if (p.kb_bf16) score_blocks<D, G, true, false, false>(p, kb_off, lo, hi, qw, fsc);
+          else score_blocks<D, G, false, false, false>(p, kb_off, lo, hi, qw, fsc);
         }
       };
       score_range(own_lo, own_hi);
-      if (n_it > 1) {
+      if (!solo) {
         if (threadIdx.x == 0) merge_todo[0] = 0u;
         __syncthreads();
         row_epoch = __builtin_amdgcn_readfirstlane(row_epoch_v);
@@ -853,8 +903,9 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         }
       }
     }
+    row_epoch = __builtin_amdgcn_readfirstlane(row_epoch_v);
     if (!staged) {  // one pass over the whole row in LDS
-      if (n_it == 1) load_q(b, h);
+      if (solo) load_q(b, h);
       __syncthreads();
       kmx = 0u;
       kmn_inv = 0u;
@@ -1508,7 +1559,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // last item to finish merges them)
   // a fused call's item keeps its partial in its workgroup's slot (the row's items
   // are consecutive workgroups), others at (row, item)
-  const int64_t pbase = SRC == kSrcTopkFused ? (int64_t)blockIdx.x : (int64_t)bh * p.max_items + item;
+  const int64_t pbase = SRC == kSrcTopkFused ? (int64_t)fused_slot : (int64_t)bh * p.max_items + item;
   for (int o = threadIdx.x; o < G * D; o += kFinThreads) {
     const int g = o / D;
     float M = kNegInf;
@@ -1571,9 +1622,9 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       __syncthreads();
       if (merge_todo[0]) {
         if (n_items_row <= kMergeGroup)
-          fused_merge_tagged<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row, partial_tag(bh, row_epoch));
+          fused_merge_tagged<D, G>(p, b, h, (int64_t)fused_slot - item, n_items_row, partial_tag(bh, row_epoch));
         else
-          fused_merge<D, G>(p, b, h, (int64_t)blockIdx.x - item, n_items_row);
+          fused_merge<D, G>(p, b, h, (int64_t)fused_slot - item, n_items_row);
       }
     }
   }

@@ -45,7 +45,7 @@ WORKLOADS = {
     "c2": dict(batch=1, hq=32, hkv=8, d=128, seq=32768, page=16, block=64, k=64, ff=1, fl=2, kv="bf16",
                k_outlier=True, seed=1235),
     "c3": dict(batch=16, hq=32, hkv=8, d=128, seq="c3", page=16, block=64, k=None, ff=0, fl=0, kv="bf16",
-               seed=1237),
+               seed=1237, pool_tokens=4 << 20),
     # the reference's own routing rule (eps threshold) at its published configuration: batch 1,
     # block 64, mixed summaries with bf16 k_bar, one suffix token, eps set so that the
     # fraction of selected blocks matches the reference's run at that length
@@ -266,7 +266,8 @@ def run_topk(name, args, dev, with_dense, with_cpu):
     lens = c3_lengths() if w["seq"] == "c3" else [w["seq"]] * w["batch"]
     w["batch"] = len(lens)
     pages_per = [math.ceil(L / w["page"]) for L in lens]
-    n_pages = sum(pages_per)
+    # the sequences' pages are drawn from a shared pool (C3: 4M tokens) in random order
+    n_pages = max(sum(pages_per), w.get("pool_tokens", 0) // w["page"])
     max_pages = max(pages_per)
     gen = torch.Generator(device=dev)
     gen.manual_seed(w["seed"])
@@ -432,7 +433,8 @@ def config_of(name, r):
             "page": w["page"], "top_k": w["k"] if w["k"] else "max(16, nb/16)",
             "forced_first": w["ff"], "forced_last": w["fl"], "kv_dtype": w["kv"],
             "k_outlier": bool(w.get("k_outlier")), "layers_rotated": r["nl"],
-            "launch": "hipgraph" if r["use_graph"] else "eager", "kv_layout": r["kv_layout"]}
+            "launch": "hipgraph" if r["use_graph"] else "eager", "kv_layout": r["kv_layout"],
+            **({"pool_tokens": w["pool_tokens"]} if w.get("pool_tokens") else {})}
 
 
 def main():

@@ -964,9 +964,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     const int n_items = max(1, (n_units + upi - 1) / upi);
     split = gridDim.x > 1 || p.rep_ml != nullptr;  // partials + merge kernel
     if (item >= n_items) {
-      // an empty slot: the merge reads every slot of the grid row
+      // an empty slot: the merge reads every slot of the grid row, (m, l) = (-inf, 0)
+      // and accumulators of zero (the merge weighs them by 0, so they must not be
+      // left undefined: 0 x NaN is NaN)
+      const int64_t slot = (int64_t)bh * p.max_items + item;
+      for (int o = threadIdx.x; o < G * D; o += kFinThreads) p.part_acc[slot * (G * D) + o] = 0.f;
       if (threadIdx.x < G) {
-        const int64_t slot = (int64_t)bh * p.max_items + item;
         p.part_ml[(slot * G + threadIdx.x) * 2 + 0] = kNegInf;
         p.part_ml[(slot * G + threadIdx.x) * 2 + 1] = 0.f;
       }

@@ -259,6 +259,39 @@ def test_condition_suffix_length_on_device(device):
         np.testing.assert_allclose(_np(out), exp, atol=TOL["bf16"], rtol=0, err_msg=f"suffix {n}")
 
 
+@pytest.mark.parametrize("case", ["few_selected", "all_selected"])
+def test_condition_decode_ignores_workspace_contents(case, device):
+    """Split-K slots of finalize items that get no units are written whole (their
+    accumulators too, which the merge weighs by 0): a workspace full of NaN bytes
+    gives the same output as a zeroed one."""
+    from interattn_amd import _native as N
+
+    # 16 blocks and one suffix tile: 17 finalize items and one route chunk, so the merge
+    # reads every slot in one round trip (empty ones included)
+    c = ("ws_nan", 23, 2, 4, 128, 64, 1000, 3, "bf16", False, "f32", False)
+    name, seed, hkv, g, d, b, p, s, *_ = c
+    announce(f"condition workspace contents: {case}")
+    host, dev = _make(c, device)
+    prefix = cb._build_prompt_blocks(dev["k"], dev["v"], b)
+    pre = _prefix_np(prefix)
+    _, mean, _ = _oracle_stats(host["q"][:, :, 0].reshape(-1, d), pre, g, False)
+    eps = _eps_list(mean)[3] if case == "few_selected" else 0.0
+    sfx_len = torch.full((1,), s, device=device, dtype=torch.int32)
+    nb = int(pre["block_valid_counts"].shape[0])
+    ws_bytes = int(N.lib().ia_condition_workspace_size(1, hkv, g, d, nb, s))
+    outs = []
+    for fill in (0, 0xFF):  # 0xFFFFFFFF is a NaN as float32
+        ws = {"condition_scratch": torch.full((max(ws_bytes, 1),), fill, device=device, dtype=torch.uint8)}
+        out, _ = cb._condition_block_decode_output(
+            q_grouped=dev["q"], prompt_prefix=prefix, k_suffix=dev["ks"], v_suffix=dev["vs"], suffix_len_dev=sfx_len,
+            block_size=b, eps=eps, prompt_len=p, attention_dtype=torch.float32, workspace=ws, collect_stats=False)
+        torch.cuda.synchronize()
+        assert ws["condition_scratch"].numel() == max(ws_bytes, 1), "the prefilled workspace was not used"
+        outs.append(out.clone())
+    assert torch.isfinite(outs[1]).all(), "NaN from an uninitialised workspace reached the output"
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_fixed_mask_hybrid_vs_oracle(dt, device):
     c = ("mask", 31, 4, 4, 128, 64, 10000, 7, dt, False, "f32", False)

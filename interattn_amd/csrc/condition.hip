@@ -2,9 +2,10 @@
 // selection rule, next to the top-k rule of select_topk.hip.
 //
 //   ia_condition_block_selection_stats  (CBT/core.py:747-814)
-//     grid = (ceil(n_chunks / 4), Hkv, batch), 256 threads; wave w owns chunk
-//     c = 4*blockIdx.x + w of 16 blocks (the reference's _SELECT_CHUNK).  Per
-//     block and query row: s = q.k_bar/sqrt(D), the range bound upper/lower
+//     grid = (n_chunks, Hkv, batch), 256 threads: workgroup c owns chunk c of 16
+//     blocks (the reference's _SELECT_CHUNK), wave w its step of 4 blocks, so each
+//     wave runs a short dependency chain and a SIMD holds several.  Per block and
+//     query row: s = q.k_bar/sqrt(D), the range bound upper/lower
 //     from the sign of q against k_max/k_min, delta = max(|upper-s|, |lower-s|),
 //     z = s + log(max(count,1)), zc = z + log cosh(delta) (or z + delta for the
 //     term1-mass-exp variant); one k_bar/k_max/k_min row per 16 lanes, DPP row
@@ -185,94 +186,104 @@ __device__ __forceinline__ void reduce_globals(const CondParams& p, int b, int h
 template <int D, int G, bool KBH, bool BDH>
 __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondParams p) {
   constexpr int DPL = D / 16;
+  __shared__ float z_lds[2][4][64];  // (z, zc) of step w at lane (r, c16) of wave w
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int step = threadIdx.x >> 6;  // wave w scores step w: blocks chunk*16 + 4w + (0..3)
   const int c16 = lane & 15;
   const int r = lane >> 4;
-  const int chunk = blockIdx.x * 4 + wave;
+  const int chunk = blockIdx.x;
   const int h = blockIdx.y;
   const int b = blockIdx.z;
-  if (chunk >= p.n_chunks) return;  // whole wave; no workgroup barrier below
 
-  // every row of the chunk first: 4 steps x 4 rows x (k_bar, k_max, k_min)
+  // this wave's four key rows (k_bar, k_max, k_min), its counts and the group's
+  // query slices, all issued before any use
   const int64_t vbase = ((int64_t)b * p.n_kv_heads + h) * p.nb;
-  int cnt[4];
-  RawRow<KBH, DPL> rb[4];
-  RawRow<BDH, DPL> rh[4], rl[4];
+  const int j = chunk * kChunk16 + 4 * step + r;
+  const bool inb = j < p.nb;
+  const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
+  RawRow<KBH, DPL> rb;
+  RawRow<BDH, DPL> rh, rl;
+  if (inb) {
+    const int64_t off = (vbase + j) * D + c16 * DPL;
+    rb.load(p.k_bar, off);
+    rh.load(p.k_max, off);
+    rl.load(p.k_min, off);
+  } else {
+    rb.zero();
+    rh.zero();
+    rl.zero();
+  }
+  // q rows h*G + g at dims c16*DPL ..: one 16-byte (bf16) or DPL/4 16-byte (f32) loads
+  u32 qw[G][DPL];
 #pragma unroll
-  for (int step = 0; step < 4; ++step) {
-    const int j = chunk * kChunk16 + 4 * step + r;
-    const bool inb = j < p.nb;
-    cnt[step] = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
-    if (inb) {
-      const int64_t off = (vbase + j) * D + c16 * DPL;
-      rb[step].load(p.k_bar, off);
-      rh[step].load(p.k_max, off);
-      rl[step].load(p.k_min, off);
+  for (int g = 0; g < G; ++g) {
+    const int64_t qo = (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL;
+    if (p.q_f32) {
+      const u32* qp = reinterpret_cast<const u32*>(p.q) + qo;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) qw[g][e] = qp[e];
     } else {
-      rb[step].zero();
-      rh[step].zero();
-      rl[step].zero();
+      const unsigned short* qp = reinterpret_cast<const unsigned short*>(p.q) + qo;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) qw[g][e] = (u32)qp[e] << 16;
     }
   }
-  float qf[G][DPL];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e)
-      qf[g][e] = q_elem(p, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL + e);
 
-  float zs[4], zcs[4];
+  const bool active = cnt > 0;
+  // upper/lower = sum q+ k_max + q- k_min / sum q+ k_min + q- k_max, i.e. with
+  // A = sum q (k_max + k_min) and B = sum |q| (k_max - k_min) >= 0:
+  // upper = (A + B)/2, lower = (A - B)/2 and delta = |A/2 - s| + B/2
+  float ksum[DPL], kdif[DPL];
 #pragma unroll
-  for (int step = 0; step < 4; ++step) {
-    const int j = chunk * kChunk16 + 4 * step + r;
-    const bool inb = j < p.nb;
-    const bool active = cnt[step] > 0;
-    // upper/lower = sum q+ k_max + q- k_min / sum q+ k_min + q- k_max, i.e. with
-    // A = sum q (k_max + k_min) and B = sum |q| (k_max - k_min) >= 0:
-    // upper = (A + B)/2, lower = (A - B)/2 and delta = |A/2 - s| + B/2
-    float ksum[DPL], kdif[DPL];
+  for (int e = 0; e < DPL; ++e) {
+    ksum[e] = rh[e] + rl[e];
+    kdif[e] = rh[e] - rl[e];
+  }
+  float ps[G], pa[G], pb[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float a = 0.f, sa = 0.f, sb = 0.f;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
-      ksum[e] = rh[step][e] + rl[step][e];
-      kdif[e] = rh[step][e] - rl[step][e];
+      const float qv = __uint_as_float(qw[g][e]);
+      a = fmaf(qv, rb[e], a);
+      sa = fmaf(qv, ksum[e], sa);
+      sb = fmaf(fabsf(qv), kdif[e], sb);
     }
-    float ps[G], pa[G], pb[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float a = 0.f, sa = 0.f, sb = 0.f;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        const float qv = qf[g][e];
-        a = fmaf(qv, rb[step][e], a);
-        sa = fmaf(qv, ksum[e], sa);
-        sb = fmaf(fabsf(qv), kdif[e], sb);
-      }
-      ps[g] = row16_sum(a);
-      pa[g] = row16_sum(sa);
-      pb[g] = row16_sum(sb);
-    }
-    // lane c16 < G finishes row g = c16
-    float sv = 0.f, av = 0.f, bv = 0.f;
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-      if (g == c16) {
-        sv = ps[g];
-        av = pa[g];
-        bv = pb[g];
-      }
-    sv *= p.scale;
-    const float dl = fabsf(0.5f * av * p.scale - sv) + 0.5f * bv * p.scale;
-    const float z = active ? sv + __logf((float)max(cnt[step], 1)) : kNegInf;
-    zs[step] = z;
-    zcs[step] = active ? (p.mass_exp ? z + dl : z + log_cosh(dl)) : kNegInf;
-    if (c16 < G && inb) {
-      const int64_t o = ((int64_t)b * (p.n_kv_heads * G) + h * G + c16) * p.nb + j;
-      p.s[o] = active ? sv : 0.f;
-      p.delta[o] = active ? dl : 0.f;
-    }
+    ps[g] = row16_sum(a);
+    pa[g] = row16_sum(sa);
+    pb[g] = row16_sum(sb);
   }
-  // chunk partials over the 16 blocks: 4 steps in-lane, 4 rows across lanes
+  // lane c16 < G finishes row g = c16
+  float sv = 0.f, av = 0.f, bv = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    if (g == c16) {
+      sv = ps[g];
+      av = pa[g];
+      bv = pb[g];
+    }
+  sv *= p.scale;
+  const float dl = fabsf(0.5f * av * p.scale - sv) + 0.5f * bv * p.scale;
+  const float z = active ? sv + __logf((float)max(cnt, 1)) : kNegInf;
+  const float zc = active ? (p.mass_exp ? z + dl : z + log_cosh(dl)) : kNegInf;
+  if (c16 < G && inb) {
+    const int64_t o = ((int64_t)b * (p.n_kv_heads * G) + h * G + c16) * p.nb + j;
+    p.s[o] = active ? sv : 0.f;
+    p.delta[o] = active ? dl : 0.f;
+  }
+  z_lds[0][step][lane] = z;
+  z_lds[1][step][lane] = zc;
+  __syncthreads();
+  if (step != 0) return;
+  // chunk partials over the 16 blocks: 4 steps in-lane, 4 rows across lanes (wave 0
+  // reads every step's values at its own lane, so the sums run in step order)
+  float zs[4], zcs[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    zs[t] = z_lds[0][t][lane];
+    zcs[t] = z_lds[1][t][lane];
+  }
   float mz = fmaxf(fmaxf(zs[0], zs[1]), fmaxf(zs[2], zs[3]));
   float mc = fmaxf(fmaxf(zcs[0], zcs[1]), fmaxf(zcs[2], zcs[3]));
   mz = rows_max(mz);
@@ -607,7 +618,7 @@ CondParams cond_params(const ia_decode_shape* shape, const void* q, const ia_blo
 
 template <int D, int G>
 void launch_stats(const CondParams& p, bool kbh, bool bdh, int batch, hipStream_t st) {
-  dim3 grid((p.n_chunks + 3) / 4, p.n_kv_heads, batch);
+  dim3 grid(p.n_chunks, p.n_kv_heads, batch);
   if (kbh) {
     if (bdh) hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, true, true>), grid, dim3(256), 0, st, p);
     else hipLaunchKernelGGL((ia_condition_block_selection_stats<D, G, true, false>), grid, dim3(256), 0, st, p);

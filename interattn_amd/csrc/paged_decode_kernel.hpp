@@ -159,7 +159,7 @@ struct DecodeParams {
   int64_t wait_ticks;
 };
 
-constexpr int kWaves = 4;  // split-K merge
+constexpr int kWaves = 8;  // split-K merge: up to kWaves x kMergeFastSlots slots in one round trip
 constexpr int kThreads = kWaves * 64;
 // finalize: one 8-wave workgroup per CU (two waves per SIMD), so the waves that
 // share a CU share one work list
@@ -1892,7 +1892,9 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
   for (int e = 0; e < PER; ++e) wsum[wave][o0 + e] = a[e];
   __syncthreads();
   for (int o = threadIdx.x; o < G * D; o += kThreads) {
-    const float t = wsum[0][o] + wsum[1][o] + wsum[2][o] + wsum[3][o];
+    float t = wsum[0][o];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) t += wsum[w][o];
     store_decode_out<G, D>(p, b, h, o, t / fmaxf(lsum[o / D], 1e-30f));
   }
 }

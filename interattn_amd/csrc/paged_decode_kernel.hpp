@@ -490,13 +490,21 @@ __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h,
   constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
   __shared__ float ml_lds[kMaxItemsPerBh][G][2];
   float acc[kMergeGroups][kMergeGroup];
+  const int ng_load = (n + kMergeGroup - 1) / kMergeGroup;
+  // one uniform branch per group of 8 slots, its loads issued back to back (slots past
+  // n re-read slot n - 1: the merge weighs them by 0)
   auto load_acc = [&](int o) {
 #pragma unroll
     for (int g = 0; g < kMergeGroups; ++g) {
+      if (g < ng_load) {
 #pragma unroll
-      for (int j = 0; j < kMergeGroup; ++j) {
-        const int s = kMergeGroup * g + j;
-        acc[g][j] = s < n ? ld_agent(p.part_acc + (slot0 + s) * (G * D) + o) : 0.f;
+        for (int j = 0; j < kMergeGroup; ++j) {
+          const int s = min(kMergeGroup * g + j, n - 1);
+          acc[g][j] = ld_agent(p.part_acc + (slot0 + s) * (G * D) + o);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMergeGroup; ++j) acc[g][j] = 0.f;
       }
     }
   };

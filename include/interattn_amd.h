@@ -388,7 +388,9 @@ IA_API int ia_sparse_topk_decode_noalloc(const ia_decode_shape* shape, const voi
  * ticks of the GPU's 100 MHz constant clock (default 2,000,000 = 20 ms; a negative
  * value restores it).  Returns the previous bound.  Applies to calls issued after
  * it on any thread.  A bound of 0 makes every waiting item compute the missing
- * parts itself (the tests use it to exercise that path).  No reference counterpart.
+ * block scores itself (the tests use it to exercise that path).  The merging item's
+ * reads of partials whose items have finished wait at least 20 ms for their stores
+ * whatever this bound.  No reference counterpart.
  */
 IA_API int64_t ia_set_wait_limit(int64_t ticks);
 

@@ -572,16 +572,20 @@ __device__ __forceinline__ u32 partial_tag(int bh, u32 row_epoch) {
 // tagged 8-byte words (value bits | tag << 32, tag = partial_tag): every
 // slot's words are loaded at once and a word whose tag has not arrived yet is read
 // again (its publisher has passed the row's counter, so its stores are in flight).
-// One merge group: the merge kernel's arithmetic, the same bits.  A word still
-// missing at the wait bound turns the output into NaN (never silent).
+// One merge group: the merge kernel's arithmetic, the same bits.  These reads wait
+// for stores already issued, so their bound is at least kMergeWaitTicks whatever the
+// caller's wait limit (which governs the score hand-off, where a fallback exists); a
+// word still missing then turns the output into NaN (never silent).
+constexpr long long kMergeWaitTicks = 2000000;  // 20 ms of the 100 MHz clock
 template <int D, int G>
 __device__ __forceinline__ void fused_merge_tagged(const DecodeParams& p, int b, int h, int64_t slot0, int n, u32 tag) {
   constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
   constexpr int W = G * D + 2 * G;                             // words per slot
   __shared__ float mlt_lds[kMergeGroup][G][2];
   const unsigned long long t0 = clock_100mhz();
+  const long long bound = max((long long)p.wait_ticks, kMergeWaitTicks);
   auto value = [&](const unsigned long long* ptr, unsigned long long v) -> float {
-    while ((u32)(v >> 32) != tag && (long long)(clock_100mhz() - t0) <= p.wait_ticks) {
+    while ((u32)(v >> 32) != tag && (long long)(clock_100mhz() - t0) <= bound) {
       __builtin_amdgcn_s_sleep(1);
       v = ld_agent_u64(ptr);
     }

@@ -530,6 +530,45 @@ def test_fused_handoff_fallback_is_exact(name, device):
         assert torch.equal(a, r) and torch.equal(b_, r)
 
 
+@pytest.mark.parametrize("rows", [(4, 32, 8), (7, 16, 4)], ids=["32rows", "28rows"])
+def test_fused_merge_item_boundary(rows, device):
+    """Uniform launches whose rows get about budget / rows items: 32 rows of 8 items on
+    a 256-workgroup launch (the tagged partials' merge, up to 8 items) and 28 rows of 9
+    (the untagged merge, more than 8).  Selection and output equal the two-step path's
+    bit for bit, also with a wait bound of 0 (every missing score computed by the
+    waiting item; the merge still waits for finished items' stores)."""
+    b, hq, hkv = rows
+    announce(f"fused merge item boundary: batch {b}, {hkv} kv heads")
+    lens = [4096] * b
+    case = make_case(seed=31 + b, batch=b, hq=hq, hkv=hkv, d=128, seq_lens=lens, page_size=16, dtype="bf16",
+                     k_outlier=False, fp8=False)
+    dev = to_dev(case, device, torch.bfloat16)
+    block, k = 64, 16
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=4096 // block, k_bar_dtype=torch.bfloat16)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], summ["k_bar"], dev["seq_lens"], k, block_size=block)
+    ref = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block)
+    ws = {}
+    outs = []
+    for limit in (None, 0):
+        previous = ia.set_wait_limit(limit) if limit is not None else None
+        try:
+            for _ in range(2):  # the second call reuses the workspace's counts and epochs
+                out, idx2, n_sel2 = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"],
+                                                          dev["seq_lens"], summ["k_bar"], k, block_size=block,
+                                                          return_selection=True, workspace=ws)
+                torch.cuda.synchronize()
+                assert torch.equal(idx2, idx) and torch.equal(n_sel2, n_sel)
+                outs.append(out.clone())
+        finally:
+            if previous is not None:
+                ia.set_wait_limit(previous)
+    for o in outs:
+        assert torch.equal(o, ref)
+    assert torch.isfinite(ref).all()
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("c", [CASES[7], CASES[2]], ids=[CASES[7][0], CASES[2][0]])
 def test_paired_kv_layout_equals_split(c, fp8, device):

@@ -51,12 +51,13 @@ WORKLOADS = {
     # the reference's own routing rule (eps threshold) at its published configuration: batch 1,
     # block 64, mixed summaries with bf16 k_bar, one suffix token, eps set so that the
     # fraction of selected blocks matches the reference's run at that length
+    # (published_fixed_us: the reference's fixed-mask path, selection skipped, same runs)
     "cond32k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=32768, block=64, frac=0.0321, suffix=1,
-                    published_us=58.78),
+                    published_us=58.78, published_fixed_us=43.14),
     "cond64k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=65536, block=64, frac=0.0155, suffix=1,
-                    published_us=68.00),
+                    published_us=68.00, published_fixed_us=44.96),
     "cond128k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=131072, block=64, frac=0.0095, suffix=1,
-                     published_us=80.41),
+                     published_us=80.41, published_fixed_us=53.97),
 }
 
 
@@ -645,6 +646,37 @@ def main_condition(args, w, dev):
     tim = spread(per_step)
     us = tim["median_us"]
 
+    # the reference's fixed-mask path (selection skipped): the same layers with layer 0's
+    # selection as the external mask (fixed_mask_hybrid_attention), also graph replays
+    fixed_mask = sel.to(torch.uint8)
+    fixed_ws = [{} for _ in layers]
+
+    def call_fixed(L, ws):
+        return cb.fixed_mask_hybrid_attention(q_grouped=L["q"], prompt_prefix=L["prefix"], selected=fixed_mask,
+                                              k_suffix=L["ks"], v_suffix=L["vs"], block_size=block,
+                                              output_dtype=torch.bfloat16, workspace=ws)
+
+    for _ in range(2):
+        for L, ws in zip(layers, fixed_ws):
+            call_fixed(L, ws)
+    torch.cuda.synchronize()
+    fixed_graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(fixed_graph):
+        fixed_outs = [call_fixed(L, ws) for L, ws in zip(layers, fixed_ws)]
+    for _ in range(3):
+        fixed_graph.replay()
+    torch.cuda.synchronize()
+    fixed_ref = [o.clone() for o in fixed_outs]
+    for o in fixed_outs:
+        o.zero_()
+    fixed_graph.replay()
+    torch.cuda.synchronize()
+    fixed_ok = all(torch.equal(o, r) for o, r in zip(fixed_outs, fixed_ref))
+    fixed_per, _ = time_repeats(fixed_graph.replay if fixed_ok else (lambda: [call_fixed(L, ws) for L, ws in
+                                                                               zip(layers, fixed_ws)]),
+                                replays, nl, stream)
+    fixed_us = spread(fixed_per)["median_us"]
+
     dense_us = None
     if not args.no_dense:
         def run_dense():
@@ -694,6 +726,12 @@ def main_condition(args, w, dev):
         "dense_us": None if dense_us is None else round(dense_us, 2),
         "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
         "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us, 2),
+        "fixed_mask": {"value": round(fixed_us, 3), "unit": "us/layer",
+                       "launch": "hipgraph" if fixed_ok else "eager",
+                       "published_us": w["published_fixed_us"],
+                       "vs_published": round(fixed_us / w["published_fixed_us"], 4),
+                       "note": "fixed_mask_hybrid_attention with this call's selection as the mask (route, "
+                               "finalize, merge; the reference's 'fixed real mask' run)"},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }

@@ -344,12 +344,20 @@ def fixed_mask_hybrid_attention(*, q_grouped, prompt_prefix, selected, k_suffix,
         raise ValueError(f"selected must have shape {(n_kv_heads, n_blocks)}, got {tuple(selected.shape)}")
     if int(block_size) != int(prompt_prefix["k_block_attn"].shape[2]):
         raise ValueError("block_size must equal the prompt block size")
-    mask = workspace_tensor(workspace, "fixed_mask", (n_kv_heads, n_blocks), device=q_grouped.device,
-                            dtype=torch.uint8)
-    mask.copy_(selected)
+    if (selected.dtype in (torch.bool, torch.uint8) and selected.is_contiguous()
+            and selected.device == q_grouped.device):
+        mask = selected.view(torch.uint8)  # read in place (one byte per block either way)
+    else:
+        mask = workspace_tensor(workspace, "fixed_mask", (n_kv_heads, n_blocks), device=q_grouped.device,
+                                dtype=torch.uint8)
+        mask.copy_(selected)
+    # the suffix length lives in device memory: one tensor per length, written once, so
+    # a captured call and later calls of another length never share it
     s_len = int(k_suffix.shape[1]) if k_suffix is not None else 0
-    sfx_len = workspace_tensor(workspace, "suffix_len", (1,), device=q_grouped.device, dtype=torch.int32)
-    sfx_len.fill_(s_len)
+    sfx_len = workspace.get(("suffix_len", s_len))
+    if sfx_len is None or sfx_len.device != q_grouped.device:
+        sfx_len = torch.full((1,), s_len, device=q_grouped.device, dtype=torch.int32)
+        workspace[("suffix_len", s_len)] = sfx_len
     out, _ = _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, sfx_len, 0.0, False, False,
                                output_dtype, workspace, mask=mask)
     return out

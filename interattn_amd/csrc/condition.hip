@@ -393,7 +393,6 @@ __device__ __forceinline__ int32_t list_entry(int j, int cnt) { return j | (cnt 
 template <int D, int G, bool VBH, bool KBH, bool MASK>
 __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   constexpr int DPL = D / 16;
-  constexpr int kUnroll = 8;  // v_bar rows in flight per lane
   __shared__ float z_lds[G][kRouteChunk];
   __shared__ float red[8][G];
   __shared__ float glob[4][G];
@@ -423,6 +422,19 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
     if (jj < p.nb) vr[t].load(p.v_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
     else vr[t].zero();
   }
+  // fixed-mask mode with bfloat16 k_bar: the k_bar rows of the same rows, issued with
+  // them (every row: the few selected ones are read and not used); float32 k_bar rows
+  // are read later, a batch at a time (registers)
+  constexpr bool kPreK = MASK && KBH;
+  RawRow<KBH, DPL> kr[kPreK ? kRows : 1];
+  if constexpr (kPreK) {
+#pragma unroll
+    for (int t = 0; t < kRows; ++t) {
+      const int jj = rc * kRouteChunk + 16 * t + 4 * wave + r;
+      if (jj < p.nb) kr[t].load(p.k_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
+      else kr[t].zero();
+    }
+  }
 
   // ---- this thread's block: count and statistics, loaded before the globals reduce
   const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
@@ -448,9 +460,7 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
   // ---- routing of this thread's block
   bool sel = false;
   if constexpr (MASK) {
-    sel = active && msel;
-#pragma unroll
-    for (int g = 0; g < G; ++g) z_lds[g][threadIdx.x] = kNegInf;  // logits computed below
+    sel = active && msel;  // (the logits are computed below)
   } else {
     float z[G], mean = 0.f;
 #pragma unroll
@@ -491,32 +501,57 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
         const float qv = q_elem(p, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL + e);
         qb[g][e] = round_if(qv, p.rep_bf16);
       }
-    __syncthreads();  // z_lds initialised
-    for (int t0 = 0; t0 < kRouteChunk / 16; t0 += kUnroll) {
-      RawRow<KBH, DPL> kr[kUnroll];
-      int cu[kUnroll];
+    // q_g . k_bar of the lane-row's blocks: the lane's partial sums of RPG rows x G
+    // query rows are reduce-scattered over the 16 lanes of the row (four DPP steps for
+    // all of them) and each complete sum goes to z_lds; the block's owner then applies
+    // the scale and log(count), or -inf for a selected or empty block
+    // (bfloat16 rows: all kRows preloaded; float32 rows: 8 at a time, so at most 8 rows
+    // per reduce-scatter)
+    constexpr int kRowsIn = KBH ? kRows : 8;                    // k_bar rows in flight
+    constexpr int NVR = G * kRowsIn >= 32 ? 32 : G * kRowsIn;  // values per reduce-scatter
+    constexpr int RPG = NVR / G;                                // rows per reduce-scatter
+    auto dots = [&](int tbase, auto&& kval) {
+      float v[NVR];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int jj = rc * kRouteChunk + 16 * (t0 + u) + 4 * wave + r;
-        const bool in2 = jj < p.nb;
-        cu[u] = in2 ? p.counts[(int64_t)b * p.nb + jj] : 0;
-        const bool rep = cu[u] > 0 && p.mask[(int64_t)bh * p.nb + jj] == 0;
-        cu[u] = rep ? cu[u] : 0;
-        if (rep) kr[u].load(p.k_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
-        else kr[u].zero();
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int jl = 16 * (t0 + u) + 4 * wave + r;
+      for (int tt = 0; tt < RPG; ++tt)
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           float a = 0.f;
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) a = fmaf(qb[g][e], round_if(kr[u][e], !KBH && p.rep_bf16), a);
-          a = row16_sum(a);
-          if (c16 == 0 && cu[u] > 0) z_lds[g][jl] = a * p.scale + __logf((float)cu[u]);
+          for (int e = 0; e < DPL; ++e) a = fmaf(qb[g][e], kval(tt, e), a);
+          v[tt * G + g] = a;
         }
+      reduce_scatter16<NVR>(v, lane);
+      const int b16 = lane & 15;
+#pragma unroll
+      for (int k = 0; k < NVR / 16; ++k) {
+        const int x = NVR == 32 ? 2 * b16 + k : b16 / (16 / NVR);  // value index held in v[k]
+        const int tt = x / G;
+        z_lds[x - tt * G][16 * (tbase + tt) + 4 * wave + r] = v[k];
       }
+    };
+    if constexpr (kPreK) {
+#pragma unroll
+      for (int t0 = 0; t0 < kRows; t0 += RPG) dots(t0, [&](int tt, int e) { return kr[t0 + tt][e]; });
+    } else {
+      for (int t0 = 0; t0 < kRows; t0 += kRowsIn) {
+        RawRow<KBH, DPL> kq[kRowsIn];
+#pragma unroll
+        for (int u = 0; u < kRowsIn; ++u) {
+          const int jj = rc * kRouteChunk + 16 * (t0 + u) + 4 * wave + r;
+          if (jj < p.nb) kq[u].load(p.k_bar, ((int64_t)bh * p.nb + jj) * D + c16 * DPL);
+          else kq[u].zero();
+        }
+#pragma unroll
+        for (int u0 = 0; u0 < kRowsIn; u0 += RPG)
+          dots(t0 + u0, [&](int tt, int e) { return round_if(kq[u0 + tt][e], p.rep_bf16); });
+      }
+    }
+    __syncthreads();  // every block's dots in z_lds
+    {  // thread t owns block t of the chunk
+      const bool rep = active && !msel;
+#pragma unroll
+      for (int g = 0; g < G; ++g) z_lds[g][threadIdx.x] = rep ? z_lds[g][threadIdx.x] * p.scale + logc : kNegInf;
     }
   }
   __syncthreads();

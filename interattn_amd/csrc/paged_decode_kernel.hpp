@@ -317,6 +317,9 @@ struct BlockScorer {
   static constexpr int NWR = DPL * EB / 4;                        // words per lane per key row
   static constexpr int NW = D >= 128 ? 64 : 32;                   // key words per lane in flight
   static constexpr int NS = NW / NWR / (QUEST ? 2 : 1);           // steps in flight (Quest reads two rows per block)
+  // whole-row scorers sum a batch's steps with one reduce-scatter; range scorers (a
+  // step or two per item) keep a row sum per step, which costs less there
+  static constexpr bool kScatter = SHARED && NS >= 4 && NS <= 32;
   using words_t = ScoreWords<D>;
 
   // the loads of every step of the batch at base that holds a block of [.., hi), without
@@ -362,19 +365,47 @@ struct BlockScorer {
     const int c16 = lane & 15;
     const int r = lane >> 4;
     auto compute = [&](int base, const words_t& wv, const float* qa, const float* qb) {
+      if constexpr (kScatter) {
+        // whole-row scoring runs full batches: the NS steps' lane shares are summed by
+        // one reduce-scatter over the 16-lane row (4 DPP rounds for all of them)
+        // instead of a row sum per step; each lane then holds whole scores
+        float v[NS];
 #pragma unroll
-      for (int t = 0; t < NS; ++t) {
-        if (base + 32 * t >= hi) break;  // uniform
-        const int j = base + 32 * t + 4 * wave + r;
-        u32 w1[NWR], w2[NWR];
+        for (int t = 0; t < NS; ++t) {
+          v[t] = 0.f;
+          if (base + 32 * t >= hi) continue;  // uniform
+          u32 w1[NWR], w2[NWR];
 #pragma unroll
-        for (int e = 0; e < NWR; ++e) {
-          w1[e] = wv[(QUEST ? 2 * t : t) * NWR + e];
-          w2[e] = QUEST ? wv[(2 * t + 1) * NWR + e] : 0u;
+          for (int e = 0; e < NWR; ++e) {
+            w1[e] = wv[(QUEST ? 2 * t : t) * NWR + e];
+            w2[e] = QUEST ? wv[(2 * t + 1) * NWR + e] : 0u;
+          }
+          v[t] = QUEST ? block_dot_quest<DPL, KBF16>(w1, w2, qa, qb) : block_dot<DPL, KBF16>(w1, qa);
         }
-        const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qa, qb, p.score_scale)
-                              : block_score<DPL, KBF16>(w1, qa, p.score_scale);
-        if (c16 == 0 && j < hi) s_lds[j] = a;
+        reduce_scatter16<NS>(v, lane);
+        constexpr int kHeld = NS >= 16 ? NS / 16 : 1;  // steps a lane holds
+        constexpr int kCopies = NS >= 16 ? 1 : 16 / NS;  // lanes holding each step
+#pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+          const int t = NS == 32 ? 2 * c16 + k : c16 / kCopies;
+          const int j = base + 32 * t + 4 * wave + r;
+          if (c16 % kCopies == 0 && base + 32 * t < hi && j < hi) s_lds[j] = v[k] * p.score_scale;
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < NS; ++t) {
+          if (base + 32 * t >= hi) break;  // uniform
+          const int j = base + 32 * t + 4 * wave + r;
+          u32 w1[NWR], w2[NWR];
+#pragma unroll
+          for (int e = 0; e < NWR; ++e) {
+            w1[e] = wv[(QUEST ? 2 * t : t) * NWR + e];
+            w2[e] = QUEST ? wv[(2 * t + 1) * NWR + e] : 0u;
+          }
+          const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qa, qb, p.score_scale)
+                                : block_score<DPL, KBF16>(w1, qa, p.score_scale);
+          if (c16 == 0 && j < hi) s_lds[j] = a;
+        }
       }
     };
     if (lo >= hi) return;

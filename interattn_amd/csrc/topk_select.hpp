@@ -36,11 +36,13 @@ __device__ __forceinline__ float key_value(u32 key) {
 
 // Score of one block row held by a 16-lane row: lane c16 owns dims c16*DPL ..
 // c16*DPL + DPL - 1 of k_bar (raw words: bf16 pairs or floats) and of the
-// group-summed query qm; the DPP row sum gives every lane the full dot product.
-// The standalone selector and the fused scorer share this arithmetic, so both
-// produce bit-identical scores.
+// group-summed query qm; block_dot is the lane's share of the dot product and the
+// DPP row sum gives every lane the full one.  The standalone selector and the fused
+// scorer share this arithmetic, so both produce bit-identical scores (the fused
+// scorer's reduce-scatter of many rows' shares adds the same pairs in the same tree
+// as row16_sum).
 template <int DPL, bool KBF16>
-__device__ __forceinline__ float block_score(const u32* w, const float* qm, float score_scale) {
+__device__ __forceinline__ float block_dot(const u32* w, const float* qm) {
   float a = 0.f;
   if constexpr (KBF16) {
 #pragma unroll
@@ -52,7 +54,12 @@ __device__ __forceinline__ float block_score(const u32* w, const float* qm, floa
 #pragma unroll
     for (int e = 0; e < DPL; ++e) a = fmaf(qm[e], __uint_as_float(w[e]), a);
   }
-  return row16_sum(a) * score_scale;
+  return a;
+}
+
+template <int DPL, bool KBF16>
+__device__ __forceinline__ float block_score(const u32* w, const float* qm, float score_scale) {
+  return row16_sum(block_dot<DPL, KBF16>(w, qm)) * score_scale;
 }
 
 // Quest score of one block (CBG/methods/quest.py:97-101): the group mean of
@@ -60,8 +67,7 @@ __device__ __forceinline__ float block_score(const u32* w, const float* qm, floa
 // (qa . k_max + qb . k_min) / G with qa = sum_g max(q_g, 0), qb = sum_g min(q_g, 0)
 // (score_scale = 1 / G).  Key rows as for block_score.
 template <int DPL, bool KBF16>
-__device__ __forceinline__ float block_score_quest(const u32* wx, const u32* wn, const float* qa, const float* qb,
-                                                   float score_scale) {
+__device__ __forceinline__ float block_dot_quest(const u32* wx, const u32* wn, const float* qa, const float* qb) {
   float a = 0.f;
   if constexpr (KBF16) {
 #pragma unroll
@@ -78,7 +84,13 @@ __device__ __forceinline__ float block_score_quest(const u32* wx, const u32* wn,
       a = fmaf(qb[e], __uint_as_float(wn[e]), a);
     }
   }
-  return row16_sum(a) * score_scale;
+  return a;
+}
+
+template <int DPL, bool KBF16>
+__device__ __forceinline__ float block_score_quest(const u32* wx, const u32* wn, const float* qa, const float* qb,
+                                                   float score_scale) {
+  return row16_sum(block_dot_quest<DPL, KBF16>(wx, wn, qa, qb)) * score_scale;
 }
 
 constexpr int kTieCands = 128;  // threshold-bucket members ranked exactly

@@ -139,21 +139,52 @@ __global__ __launch_bounds__(kSelThreads) void ia_condition_block_select_topk(Se
       }
       have_qm = true;
     }
+    if constexpr (NS >= 4 && NS <= 32) {
+      // the NS steps' lane shares summed by one reduce-scatter over the 16-lane row
+      // (the same pairs in the same tree as block_score's row sum, so the same bits)
+      float v[NS];
 #pragma unroll
-    for (int t = 0; t < NS; ++t) {
-      if (base + kRowsPerStep * t >= nb) break;  // uniform
-      u32 w1[NWR], w2[NWR];
+      for (int t = 0; t < NS; ++t) {
+        v[t] = 0.f;
+        if (base + kRowsPerStep * t >= nb) continue;  // uniform
+        u32 w1[NWR], w2[NWR];
 #pragma unroll
-      for (int e = 0; e < NWR; ++e) {
-        w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
-        w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
+        for (int e = 0; e < NWR; ++e) {
+          w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
+          w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
+        }
+        v[t] = QUEST ? block_dot_quest<DPL, KBF16>(w1, w2, qm, qn) : block_dot<DPL, KBF16>(w1, qm);
       }
-      const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qm, qn, p.score_scale)
-                            : block_score<DPL, KBF16>(w1, qm, p.score_scale);
-      const int j = base + kRowsPerStep * t + 4 * wave + r;
-      if (c16 == 0 && j < nb) {
-        if (in_lds) sc_lds[j] = a;
-        if (sc_row) sc_row[j] = a;
+      reduce_scatter16<NS>(v, lane);
+      constexpr int kHeld = NS >= 16 ? NS / 16 : 1;    // steps a lane holds
+      constexpr int kCopies = NS >= 16 ? 1 : 16 / NS;  // lanes holding each step
+#pragma unroll
+      for (int k = 0; k < kHeld; ++k) {
+        const int t = NS == 32 ? 2 * c16 + k : c16 / kCopies;
+        const int j = base + kRowsPerStep * t + 4 * wave + r;
+        if (c16 % kCopies == 0 && base + kRowsPerStep * t < nb && j < nb) {
+          const float a = v[k] * p.score_scale;
+          if (in_lds) sc_lds[j] = a;
+          if (sc_row) sc_row[j] = a;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NS; ++t) {
+        if (base + kRowsPerStep * t >= nb) break;  // uniform
+        u32 w1[NWR], w2[NWR];
+#pragma unroll
+        for (int e = 0; e < NWR; ++e) {
+          w1[e] = w[(QUEST ? 2 * t : t) * NWR + e];
+          w2[e] = QUEST ? w[(2 * t + 1) * NWR + e] : 0u;
+        }
+        const float a = QUEST ? block_score_quest<DPL, KBF16>(w1, w2, qm, qn, p.score_scale)
+                              : block_score<DPL, KBF16>(w1, qm, p.score_scale);
+        const int j = base + kRowsPerStep * t + 4 * wave + r;
+        if (c16 == 0 && j < nb) {
+          if (in_lds) sc_lds[j] = a;
+          if (sc_row) sc_row[j] = a;
+        }
       }
     }
   }

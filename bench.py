@@ -80,7 +80,7 @@ def parse():
     ap.add_argument("--kv-layout", default="paired", choices=["split", "paired", "head_paired"],
                     help="K/V pool layout: K and V of a (page, kv head) adjacent in one buffer (paired: "
                          "one 8 KiB run per bf16 page and head), or separate K and V pools (split)")
-    ap.add_argument("--extra", default="c5,c3,c2",
+    ap.add_argument("--extra", default="c5,c3,c2,cond32k,cond64k,cond128k",
                     help="other BASELINE configs timed in the same run and reported under 'extra' "
                          "(comma list; empty for none)")
     return ap.parse_args()
@@ -269,6 +269,18 @@ def cpu_baseline(w, L0, table, lens, k_cap, gpu_out, runs=5):
     return times[len(times) // 2] * 1e6, times, err
 
 
+def settle(run, nl, ms):
+    """Untimed passes for ``ms`` milliseconds of sustained load; returns (ms, steps)."""
+    steps = 0
+    t_s = time.perf_counter()
+    while (time.perf_counter() - t_s) * 1e3 < ms:
+        for _ in range(8):
+            run()
+        torch.cuda.synchronize()
+        steps += 8 * nl
+    return (time.perf_counter() - t_s) * 1e3, steps
+
+
 def run_topk(name, args, dev, with_dense, with_cpu):
     """Time one top-k workload; returns the result dict (the JSON line's fields)."""
     w = dict(WORKLOADS[name])
@@ -351,16 +363,10 @@ def run_topk(name, args, dev, with_dense, with_cpu):
 
     timed_graph = args.launch == "graph" and use_graph
     # settle: under sustained load the per-call time falls by 4-6% over the first
-    # 0.1-0.2 s (same code, same bits; the GPU's power state ramping), so untimed calls
-    # run until args.settle_ms of load has passed and the timed steps see the steady state
-    settle_steps = 0
-    t_s = time.perf_counter()
-    while (time.perf_counter() - t_s) * 1e3 < args.settle_ms:
-        for _ in range(8):
-            (run_replay if timed_graph else run_call)()
-        torch.cuda.synchronize()
-        settle_steps += 8 * nl
-    settle_ms = (time.perf_counter() - t_s) * 1e3
+    # 0.1-0.2 s (same code, same bits, sclk and mclk reading the same before and after),
+    # so untimed calls run until args.settle_ms of load has passed and the timed steps
+    # see the steady state
+    settle_ms, settle_steps = settle(run_replay if timed_graph else run_call, nl, args.settle_ms)
     t0 = time.perf_counter()
     per_step, steps = time_repeats(run_replay if timed_graph else run_call, replays, nl, stream)
     wall = time.perf_counter() - t0
@@ -468,13 +474,20 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if w.get("mode") == "cond":
-        return main_condition(args, w, dev)
+        line = run_condition(args, w, dev, with_dense=not args.no_dense, with_cpu=not args.no_cpu_baseline)
+        print(json.dumps(line), flush=True)
+        return
     name = args.workload
     r = run_topk(name, args, dev, with_dense=not args.no_dense, with_cpu=not args.no_cpu_baseline)
     copy_gbps = copy_ceiling_gbps(dev)
     traffic, traffic_src = traffic_of(name)
     extra = {}
     for other in [x for x in args.extra.split(",") if x and x != name]:
+        if WORKLOADS[other].get("mode") == "cond":
+            c = run_condition(args, dict(WORKLOADS[other]), dev, with_dense=False, with_cpu=False)
+            extra[other] = {k: c[k] for k in ("config", "value", "unit", "vs_baseline", "baseline_note", "timing",
+                                              "achieved_GBps", "fixed_mask")}
+            continue
         e = run_topk(other, args, dev, with_dense=False, with_cpu=False)
         t_o, _ = traffic_of(other)
         extra[other] = {"config": config_of(other, e), "value": e["us"], "unit": "us/layer", "timing": e["timing"],
@@ -580,9 +593,10 @@ def condition_cpu_baseline(w, L, eps):
     return (time.perf_counter() - t0) / reps * 1e6, reps
 
 
-def main_condition(args, w, dev):
+def run_condition(args, w, dev, with_dense, with_cpu):
     """One decode-attention layer call of the reference's condition path
-    (``_condition_block_decode_output`` with the fused HIP finalize), batch 1."""
+    (``_condition_block_decode_output`` with the fused HIP finalize), batch 1; returns
+    the JSON line."""
     from interattn_amd import condition_block as cb
 
     hkv, g, d, block, p, s = w["hkv"], w["hq"] // w["hkv"], w["d"], w["block"], w["seq"], w["suffix"]
@@ -655,10 +669,12 @@ def main_condition(args, w, dev):
             for L in layers:
                 call(L)
 
+    settle_ms, settle_steps = settle(run_replay, nl, args.settle_ms)
     t0 = time.perf_counter()
     per_step, steps = time_repeats(run_replay, replays, nl, stream)
     wall = time.perf_counter() - t0
     tim = spread(per_step)
+    tim["settle"] = {"ms": round(settle_ms, 1), "steps": settle_steps}
     us = tim["median_us"]
 
     # the reference's fixed-mask path (selection skipped): the same layers with layer 0's
@@ -693,7 +709,7 @@ def main_condition(args, w, dev):
     fixed_us = spread(fixed_per)["median_us"]
 
     dense_us = None
-    if not args.no_dense:
+    if with_dense:
         def run_dense():
             for L in layers:
                 cb._sdpa_full_attention_forward(None, L["q"].view(1, w["hq"], 1, d), L["k"][None], L["v"][None],
@@ -704,7 +720,7 @@ def main_condition(args, w, dev):
     dense_bytes = qo_b + hkv * p * d * 2 * 2
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if with_cpu:
         cpu_us, reps = condition_cpu_baseline(w, layers[0], eps)
         cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
                "sample": f"one full layer call (batch 1), {reps} reps: numpy oracle of the eager selection and "
@@ -750,7 +766,7 @@ def main_condition(args, w, dev):
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }
-    print(json.dumps(line), flush=True)
+    return line
 
 
 if __name__ == "__main__":

@@ -453,6 +453,18 @@ def traffic_of(name):
     return None, None
 
 
+def kernel_avg_of(name, total_bytes):
+    """The dominant kernel's rocprofv3 trace average (profiles/hbm_traffic.json, taken
+    over the same settled calls) and the roofline fraction it gives on its own."""
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    rec = json.load(open(tpath)).get(name) if os.path.exists(tpath) else None
+    if not rec or not rec.get("kernel_avg_us"):
+        return {}
+    avg = float(rec["kernel_avg_us"])
+    return {"rocprof_kernel_avg_us": avg,
+            "rocprof_kernel_frac": round(total_bytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def config_of(name, r):
     w, lens = r["w"], r["lens"]
     return {"workload": f"BASELINE config {name[1:]}", "batch": len(lens),
@@ -527,6 +539,7 @@ def main():
                      "achieved": round(r["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(r["gbps"] / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "traffic_source": traffic_src,
+                     **kernel_avg_of(name, r["total_bytes"]),
                      "timed": "the same median per-step time as value (one kernel launch per step: the "
                               "dominant kernel's own time plus the launch gap)"},
         "two_step_finalize_GBps": round(r["fin_bytes"] / (r["fin_us"] * 1e-6) / 1e9, 1),

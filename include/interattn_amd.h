@@ -365,14 +365,17 @@ IA_API int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, co
  * device memory (code under HIP graph capture, serving loops that forbid
  * allocation): the call allocates nothing (no hipMalloc, hipFree or allocating
  * library routine).  The buffer is a static device array of
- * IA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call whose
- * ia_sparse_topk_decode workspace would exceed it fails with IA_ERR_WORKSPACE.
+ * IA_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call of more
+ * than 2048 (sequence, kv head) rows, or whose workspace (its rows' part at the
+ * buffer's start counted as 2048 rows) would exceed the buffer, fails with
+ * IA_ERR_WORKSPACE.
  * Every call on a GPU shares that GPU's buffer, which keeps state from call to
- * call: when the call shape (batch, heads, head_dim, nb_max, k_cap, block_size)
- * differs from the previous call's on that device, a clear kernel runs first on
- * `stream` (also inside a graph being captured, where it becomes a node of the
- * graph).  Calls that overlap on one GPU race, and so does replaying a captured
- * graph holding this call between calls of another shape.  Results equal
+ * call (per-row counts and epochs; every published word carries its row's tag),
+ * so calls of different shapes may follow each other in any order, also as graph
+ * replays between eager calls.  The first call on a device runs a clear kernel of
+ * the whole buffer on `stream` first (inside a graph being captured it becomes a
+ * node of the graph, so every replay clears, and the next call outside the graph
+ * clears again).  Calls that overlap on one GPU race.  Results equal
  * ia_sparse_topk_decode's, bit for bit.
  */
 #define IA_NOALLOC_SCRATCH_BYTES (16u << 20)

@@ -208,11 +208,12 @@ int64_t fused_grid_bound(int64_t rows, int g, int d, int k_cap, int block_size) 
   return std::max<int64_t>(std::max<int64_t>(resident, rows), rows * ((s_cap + t_cap - 1) / t_cap));
 }
 
-FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size) {
+FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size,
+                        int64_t row_lines) {
   const int64_t rows = (int64_t)batch * hkv;
   FusedWs L;
   L.slots = fused_grid_bound(rows, g, d, k_cap, block_size);
-  L.sbuf = align_up((size_t)rows * kFlagStride * 4, 256);
+  L.sbuf = align_up((size_t)std::max(rows, row_lines) * kFlagStride * 4, 256);
   L.part_ml = align_up(L.sbuf + (size_t)rows * std::max(nb_max, 1) * 8, 256);
   L.part_acc = align_up(L.part_ml + (size_t)L.slots * g * 2 * 4, 256);
   L.part_n = align_up(L.part_acc + (size_t)L.slots * g * d * 4, 256);
@@ -225,7 +226,7 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
                     const ia_block_keys* keys, int32_t block_size, int32_t nb_max, int32_t k,
                     const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
                     int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out,
-                    void* workspace, size_t workspace_bytes, void* stream) {
+                    void* workspace, size_t workspace_bytes, void* stream, int64_t row_lines) {
   int rc = check_shape(shape);
   if (rc) return rc;
   rc = check_kv(kv, shape->head_dim);
@@ -246,7 +247,7 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
     return fail(IA_ERR_UNSUPPORTED, "fused top-k decode takes nb_max <= " + std::to_string(kFusedMaxBlocks) +
                                         " and k_cap <= " + std::to_string(kMaxUnitsPerItem) +
                                         "; use ia_select_topk + ia_sparse_paged_decode");
-  const FusedWs L = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, block_size);
+  const FusedWs L = fused_ws_layout(shape->batch, shape->n_kv_heads, G, D, nb_max, k_cap, block_size, row_lines);
   if (!workspace || workspace_bytes < L.total)
     return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(L.total) + " bytes");
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");

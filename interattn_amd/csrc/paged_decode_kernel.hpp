@@ -591,12 +591,14 @@ __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h,
   }
 }
 
-// A workgroup's split-K slot serves whichever row the launch plan gives it, so the
-// tag of a tagged partial names the row too: row << 19 | (epoch + 1) mod 2^19 (rows
-// < 2^13).  A slot's earlier contents then never match unless they are 2^19 calls
-// of the same row old.
+// Tag of a row's published words (score entries and tagged partials): a slot or an
+// entry serves whichever row the launch plan (and the call shape) gives it, so the
+// tag names the row too: row << 19 | (epoch mod (2^19 - 1)) + 1 (rows < 2^13).  The
+// low part is never 0, so a zero-filled word never matches, and the row's epoch only
+// grows (it is never reset between calls of any shape), so a word left by an earlier
+// call of any row never matches unless it is 2^19 - 1 split calls of the same row old.
 __device__ __forceinline__ u32 partial_tag(int bh, u32 row_epoch) {
-  return ((u32)bh << 19) | ((row_epoch + 1u) & 0x7ffffu);
+  return ((u32)bh << 19) | ((row_epoch % 0x7ffffu) + 1u);
 }
 
 // The merge of a row of at most kMergeGroup items whose partials were published as
@@ -841,8 +843,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   if constexpr (SRC == kSrcTopkFused) {
     // ---- block scores: item i of the row's n scores blocks [i nbs / n, (i+1) nbs / n)
     // into LDS and publishes them as tagged 8-byte entries, score bits | tag << 32 with
-    // tag = the row's epoch + 1 (the epoch counts the calls that split the row, so an
-    // entry left by an earlier call never matches).  Each item takes the other items'
+    // tag = partial_tag(row, epoch) (the epoch counts the calls that split the row, so
+    // an entry left by an earlier call, of this row or another, never matches).  Each item takes the other items'
     // blocks from the entries whose tag has arrived; when one is still missing at the
     // wait bound, it scores the other items' blocks itself (same arithmetic, same
     // bits).  Every item then holds the whole row and applies the shared top-k rule
@@ -912,7 +914,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         if (threadIdx.x == 0) merge_todo[0] = 0u;
         __syncthreads();
         row_epoch = __builtin_amdgcn_readfirstlane(row_epoch_v);
-        const u32 tag = row_epoch + 1u;
+        const u32 tag = partial_tag(bh, row_epoch);
         for (int j = own_lo + threadIdx.x; j < own_hi; j += kFinThreads) {
           const float sc = fsc[j];
           st_agent_u64(row_entries + j, ((unsigned long long)tag << 32) | __float_as_uint(sc));
@@ -2000,20 +2002,26 @@ int decode_items(const DecodeParams& p, int kv_dtype, int d, int g, int src, int
                  int nsub_u, int cap_items, hipStream_t st, int* items_out);
 
 // Fused top-k decode workspace: one 256-byte line per row first (the row's
-// finished-partial count, zero between calls, and its epoch), then the published
-// score entries [row, nb_max] (8 bytes each), then the split-K partials, one slot
-// per workgroup ((m, l) [slot, G, 2], acc [slot, G, D]) and the items per row.
-// The part before part_ml carries state from call to call (zero-filled at first).
+// finished-partial count, zero between calls, and its epoch; max(rows, row_lines)
+// lines), then the published score entries [row, nb_max] (8 bytes each), then the
+// split-K partials, one slot per workgroup ((m, l) [slot, G, 2], acc [slot, G, D])
+// and the items per row.  Zero-filled once; the row lines then carry the counts and
+// epochs from call to call, and every published word carries its row's tag
+// (partial_tag).  A buffer whose row lines stay at one place for every shape (a
+// fixed row_lines at least every call's rows) may therefore serve calls of any shape
+// in turn without another clear; with row_lines = 0 the later parts start where the
+// shape's own rows end, so the buffer belongs to one shape.
 struct FusedWs {
   size_t sbuf, part_ml, part_acc, part_n, tpart, total;
   int64_t slots;
 };
-FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size);
+FusedWs fused_ws_layout(int batch, int hkv, int g, int d, int nb_max, int k_cap, int block_size,
+                        int64_t row_lines = 0);
 int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_kv* kv, const int32_t* seq_lens,
                     const ia_block_keys* keys, int32_t block_size, int32_t nb_max, int32_t k,
                     const int32_t* k_per_seq, int32_t forced_first, int32_t forced_last, int32_t forced_in_k,
                     int32_t k_cap, float scale, void* out, int32_t out_dtype, int32_t* idx_out, int32_t* n_sel_out,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    void* workspace, size_t workspace_bytes, void* stream, int64_t row_lines = 0);
 
 // Block-keys descriptor check and score scale (select_topk.hip); the hand-off wait
 // bound of the fused top-k call (paged_decode.hip).

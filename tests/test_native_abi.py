@@ -107,3 +107,18 @@ def test_noalloc_rejects_bad_arguments_before_its_scratch():
     rc = lib.ia_sparse_topk_decode_noalloc(sh, 256, kv, 256, keys, 64, 8, 4, None, 0, 0, 0, 4, 1.0, 256, N.IA_BF16,
                                            None, None, None)
     assert rc != 0
+
+
+def test_noalloc_rejects_calls_beyond_its_scratch_before_launching():
+    # more (sequence, kv head) rows than the scratch's fixed row lines, then rows that
+    # fit but a score row too long for the bytes: both rejected before any launch
+    lib = N.lib()
+    keys = N.BlockKeys(score=N.IA_SCORE_MEAN_KEY, dtype=N.IA_BF16, k_bar=256)
+    kv = N.PagedKV()
+    for batch, nb_max, what in ((300, 64, "rows"), (256, 4096, "bytes")):
+        sh = N.DecodeShape(batch=batch, n_q_heads=32, n_kv_heads=8, head_dim=128, q_batch_stride=32 * 128,
+                           q_row_stride=128, q_dtype=N.IA_BF16)
+        rc = lib.ia_sparse_topk_decode_noalloc(sh, 256, kv, 256, keys, 128, nb_max, 16, None, 0, 0, 0, 64, 0.1, 256,
+                                               N.IA_BF16, None, None, None)
+        assert rc == N.IA_ERR_WORKSPACE, (what, lib.ia_last_error())
+        assert "scratch" in lib.ia_last_error().decode(), what

@@ -11,9 +11,11 @@ BASELINE config 4: batch 16, 131072-token contexts, 32 query / 8 KV heads, head_
 128, KV block 128, top-64 blocks per KV head, bf16 K/V in a paged pool of 16-token
 pages in randomly permuted order, bf16 k_bar summaries.  Inputs are synthetic
 (q, K, V ~ N(0,1)), resident in HBM before timing starts; by default K and V of a
-(page, kv head) sit next to each other in one buffer (``--kv-layout``).  ``--layers`` independent
-pools are rotated through so consecutive calls never re-read the same K/V pages
-(the 256 MB MALL cannot hold the per-call working set).
+(page, kv head) sit next to each other in one buffer (``--kv-layout``).  Independent
+layers (pools, queries and summaries) are rotated through so that no call finds its
+block summaries or K/V pages in the 256 MB MALL: by default at least 8 layers, and as
+many as it takes for the rotation's touched bytes to exceed 512 MiB (``--layers``
+overrides).
 
 Prints one JSON line (see the keys below).  ``--gpus`` above 1 is rejected: this
 build runs on one GPU.
@@ -53,11 +55,11 @@ WORKLOADS = {
     # fraction of selected blocks matches the reference's run at that length
     # (published_fixed_us: the reference's fixed-mask path, selection skipped, same runs)
     "cond32k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=32768, block=64, frac=0.0321, suffix=1,
-                    published_us=58.78, published_fixed_us=43.14),
+                    published_us=58.78, published_fixed_us=43.14, published_io_frac=0.153),
     "cond64k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=65536, block=64, frac=0.0155, suffix=1,
-                    published_us=68.00, published_fixed_us=44.96),
+                    published_us=68.00, published_fixed_us=44.96, published_io_frac=0.173),
     "cond128k": dict(mode="cond", batch=1, hq=32, hkv=8, d=128, seq=131072, block=64, frac=0.0095, suffix=1,
-                     published_us=80.41, published_fixed_us=53.97),
+                     published_us=80.41, published_fixed_us=53.97, published_io_frac=0.221),
 }
 
 
@@ -67,7 +69,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c4", choices=sorted(WORKLOADS))
-    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--layers", type=int, default=None,
+                    help="independent layers rotated through (default: at least 8, and enough that the "
+                         "rotation touches more than 512 MiB, twice the MALL)")
     ap.add_argument("--launch", default="stream", choices=["stream", "graph"],
                     help="how the timed layer calls are launched: back-to-back on the stream (the library's "
                          "call path, default) or as hipGraph replays; the other path is timed too and reported "
@@ -84,6 +88,29 @@ def parse():
                     help="other BASELINE configs timed in the same run and reported under 'extra' "
                          "(comma list; empty for none)")
     return ap.parse_args()
+
+
+MALL_BYTES = 256 << 20
+
+
+def rotation_layers(args, per_call_bytes):
+    """Layers to rotate: ``--layers`` if given, else max(8, the count whose touched bytes
+    exceed twice the 256 MB MALL), so every call reads its summaries and K/V cold."""
+    if args.layers:
+        return args.layers
+    return int(min(64, max(8, math.ceil(2 * MALL_BYTES / max(per_call_bytes, 1)))))
+
+
+def topk_bytes_estimate(w, lens):
+    """Touched bytes of one top-k layer call (k_bar rows + the selected blocks' K/V),
+    before the selection is known: every row selects its k (or k_i) blocks."""
+    s_kv = 1 if w["kv"] == "fp8" else 2
+    tot = 0
+    for L in lens:
+        nb = math.ceil(L / w["block"])
+        k = w["k"] if w["k"] else max(16, nb // 16)
+        tot += w["hkv"] * (nb * w["d"] * 2 + min(nb, k + w["ff"] + w["fl"]) * w["block"] * w["d"] * 2 * s_kv)
+    return tot
 
 
 def c3_lengths():
@@ -305,9 +332,10 @@ def run_topk(name, args, dev, with_dense, with_cpu):
         kvec = torch.tensor(ks, device=dev, dtype=torch.int32)
         k_cap = max(ks) + w["ff"] + w["fl"]
     t_setup = time.perf_counter()
-    layers = [make_layer(w, dev, gen, lens, table, n_pages, args.kv_layout) for _ in range(args.layers)]
+    n_layers = rotation_layers(args, topk_bytes_estimate(w, lens))
+    layers = [make_layer(w, dev, gen, lens, table, n_pages, args.kv_layout) for _ in range(n_layers)]
     torch.cuda.synchronize()
-    print(f"[bench] workload={name} layers={args.layers} setup {time.perf_counter() - t_setup:.1f}s",
+    print(f"[bench] workload={name} layers={n_layers} setup {time.perf_counter() - t_setup:.1f}s",
           file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream()
@@ -496,9 +524,11 @@ def main():
     extra = {}
     for other in [x for x in args.extra.split(",") if x and x != name]:
         if WORKLOADS[other].get("mode") == "cond":
-            c = run_condition(args, dict(WORKLOADS[other]), dev, with_dense=False, with_cpu=False)
+            c = run_condition(args, dict(WORKLOADS[other]), dev, with_dense=not args.no_dense,
+                              with_cpu=not args.no_cpu_baseline)
             extra[other] = {k: c[k] for k in ("config", "value", "unit", "vs_baseline", "baseline_note", "timing",
-                                              "achieved_GBps", "fixed_mask")}
+                                              "achieved_GBps", "pct_hbm_peak", "fixed_mask", "dense_and_io_model",
+                                              "cpu_baseline")}
             continue
         e = run_topk(other, args, dev, with_dense=False, with_cpu=False)
         t_o, _ = traffic_of(other)
@@ -572,38 +602,50 @@ def pick_eps(cb, L, w, frac):
     return best[1]
 
 
-def condition_cpu_baseline(w, L, eps):
-    """The oracle (numpy restatement of the reference's CPU path: eager selection
-    ``_select_prompt_blocks_eager`` + dense hybrid attention
-    ``_condition_block_decode_output_dense``) on one full layer call."""
-    import numpy as np
+def condition_cpu_baseline(w, L, eps, gpu_out, runs=5):
+    """The reference's CPU PyTorch path for its own rule on the host cores: the eager
+    selection ``_select_prompt_blocks_eager`` (CBT/core.py:509-555) and the dense
+    hybrid attention ``_condition_block_decode_output_dense`` (CBT/legacy.py:797-868)
+    of one full layer call, restated in float32 torch (``oracle.torch_path``, pinned
+    against the reference's golden vectors), bf16 K/V widened inside the call as the
+    reference does.  Median of ``runs`` timed calls after one warm-up call; also
+    returns the largest difference from the GPU output."""
+    from oracle import torch_path as T
 
-    from oracle import attention as A
-    from oracle import select as S
-
-    q = L["q"].float().cpu().numpy()
-    k = L["k"].float().cpu().numpy()
-    v = L["v"].float().cpu().numpy()
-    ks = L["ks"].float().cpu().numpy()
-    vs = L["vs"].float().cpu().numpy()
-    pre = {key: (L["prefix"][key].float() if L["prefix"][key].is_floating_point() else L["prefix"][key]).cpu().numpy()
-           for key in ("k_bar", "v_bar", "k_max", "k_min", "v_norm_max", "v_norm_all", "block_valid_counts")}
+    cpu = torch.device("cpu")
     b = w["block"]
-    p = k.shape[1]
-    nb = pre["block_valid_counts"].shape[0]
-    kb = np.concatenate([k, np.zeros((k.shape[0], nb * b - p, k.shape[2]), k.dtype)], 1).reshape(k.shape[0], nb, b, -1)
-    vb = np.concatenate([v, np.zeros((v.shape[0], nb * b - p, v.shape[2]), v.dtype)], 1).reshape(v.shape[0], nb, b, -1)
-    tok = np.arange(nb * b).reshape(nb, b)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        sel, z = S.select_condition_eager(q, pre, eps)
-        A.hybrid_decode_dense(q, kb, vb, tok < p, tok, p + ks.shape[1] - 1, p, ks, vs, sel, z, pre["v_bar"],
-                              pre["block_valid_counts"] > 0)
-        reps += 1
-        if time.perf_counter() - t0 > 10.0 or reps >= 20:
-            break
-    return (time.perf_counter() - t0) / reps * 1e6, reps
+    k = L["k"].to(cpu)
+    v = L["v"].to(cpu)
+    hkv, p, d = k.shape
+    nb = math.ceil(p / b)
+    pad = lambda x: torch.cat([x, x.new_zeros((hkv, nb * b - p, d))], 1).view(hkv, nb, b, d)  # noqa: E731
+    kb, vb = pad(k), pad(v)
+    pre = {key: L["prefix"][key].to(cpu) for key in ("k_bar", "v_bar", "k_max", "k_min", "v_norm_max",
+                                                     "block_valid_counts")}
+    q, ks, vs = L["q"].to(cpu), L["ks"].to(cpu), L["vs"].to(cpu)
+
+    def one():
+        t0 = time.perf_counter()
+        out, _ = T.condition_layer_call(q, pre, kb, vb, ks, vs, eps)
+        return time.perf_counter() - t0, out
+
+    _, out = one()
+    times = sorted(one()[0] for _ in range(runs))
+    err = float((out - gpu_out.float().cpu()).abs().max())
+    return times[len(times) // 2] * 1e6, times, err
+
+
+def io_model(sel, counts, p, s):
+    """The reference's optimistic IO model (CBG/real_attention_benchmark/run.py:147-159),
+    in vectors read: dense 2 (P + S); sparse 3 per non-empty block (k_bar, k_max,
+    k_min), one v_bar per unselected non-empty block, 2 per selected token and 2 per
+    suffix token, with the selected and representative counts averaged over kv heads."""
+    active = counts > 0
+    sel_tokens = (sel.long() * counts[None].long()).sum(1).float().mean().item()
+    reps = ((~sel) & active[None]).sum(1).float().mean().item()
+    full = 2.0 * (p + s)
+    sparse = 3.0 * float(active.sum().item()) + reps + 2.0 * sel_tokens + 2.0 * s
+    return full / sparse
 
 
 def run_condition(args, w, dev, with_dense, with_cpu):
@@ -615,8 +657,13 @@ def run_condition(args, w, dev, with_dense, with_cpu):
     hkv, g, d, block, p, s = w["hkv"], w["hq"] // w["hkv"], w["d"], w["block"], w["seq"], w["suffix"]
     gen = torch.Generator(device=dev)
     gen.manual_seed(1238)
+    nb_est = math.ceil(p / block)
+    # touched bytes of one call: the three summary rows of every block, v_bar of the
+    # unselected ones and the selected blocks' K/V
+    per_call = hkv * nb_est * d * 2 * 4 + int(w["frac"] * hkv * p * d * 2 * 2)
+    n_layers = rotation_layers(args, per_call)
     layers = []
-    for _ in range(args.layers):
+    for _ in range(n_layers):
         L = {name: torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen)
              for name, shape in (("k", (hkv, p, d)), ("v", (hkv, p, d)), ("ks", (hkv, s, d)), ("vs", (hkv, s, d)),
                                  ("q", (hkv, g, 1, d)))}
@@ -722,23 +769,47 @@ def run_condition(args, w, dev, with_dense, with_cpu):
     fixed_us = spread(fixed_per)["median_us"]
 
     dense_us = None
+    dense = None
     if with_dense:
+        # the dense fallback on the same layers (the HF-signature dense entry point,
+        # _sdpa_full_attention_forward -> the HIP dense paged decode over the whole
+        # context), as graph replays like the sparse call
         def run_dense():
             for L in layers:
                 cb._sdpa_full_attention_forward(None, L["q"].view(1, w["hq"], 1, d), L["k"][None], L["v"][None],
                                                 None, d ** -0.5)
         run_dense()
         torch.cuda.synchronize()
-        dense_us = time_events(run_dense, 5, stream) * 1e3 / nl
+        dense_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(dense_graph):
+            run_dense()
+        dense_graph.replay()
+        torch.cuda.synchronize()
+        per_d, _ = time_repeats(dense_graph.replay, max(3, replays // 4), nl, stream)
+        dense_us = spread(per_d)["median_us"]
+        io_ideal = io_model(sel, counts, p, s)
+        dense = {"dense_us": round(dense_us, 2), "sparse_vs_dense_speedup": round(dense_us / us, 3),
+                 "io_ideal_speedup": round(io_ideal, 3),
+                 "fraction_of_io_ideal": round(dense_us / us / io_ideal, 4),
+                 "published_fraction_of_io_ideal": w["published_io_frac"],
+                 "note": "dense = the HIP dense paged decode over the whole context (hipGraph replays); "
+                         "io_ideal_speedup = the reference's optimistic IO model "
+                         "(CBG/real_attention_benchmark/run.py:147-159) on this call's selection; "
+                         "fraction_of_io_ideal = (dense / sparse) / io_ideal_speedup, as the reference reports"}
+        del dense_graph
     dense_bytes = qo_b + hkv * p * d * 2 * 2
 
     cpu = None
     if with_cpu:
-        cpu_us, reps = condition_cpu_baseline(w, layers[0], eps)
-        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": 1, "kind": "port",
-               "sample": f"one full layer call (batch 1), {reps} reps: numpy oracle of the eager selection and "
-                         f"the dense hybrid attention (single-threaded numpy)",
-               "cpu": cpu_model()}
+        out0 = call(layers[0])[0].clone()
+        torch.cuda.synchronize()
+        cpu_us, cpu_runs, cpu_err = condition_cpu_baseline(w, layers[0], eps, out0)
+        cpu = {"value": round(cpu_us, 1), "unit": "us/layer", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"one full layer call (batch 1): the reference's eager selection and dense hybrid "
+                         f"attention restated in float32 torch on the host cores (oracle/torch_path.py, "
+                         f"condition_layer_call); median of {len(cpu_runs)} calls after one warm-up call "
+                         f"(min {min(cpu_runs) * 1e6:.0f}, max {max(cpu_runs) * 1e6:.0f} us)",
+               "cpu": cpu_model(), "os_cpu_count": os.cpu_count(), "max_abs_diff_vs_gpu": round(cpu_err, 6)}
     gbps = total / (us * 1e-6) / 1e9
     line = {
         "metric": "\u00b5s per decode-attn layer + achieved HBM GB/s (% peak), 32K\u2013128K ctx",
@@ -770,6 +841,7 @@ def run_condition(args, w, dev, with_dense, with_cpu):
         "dense_us": None if dense_us is None else round(dense_us, 2),
         "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
         "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us, 2),
+        "dense_and_io_model": dense,
         "fixed_mask": {"value": round(fixed_us, 3), "unit": "us/layer",
                        "launch": "hipgraph" if fixed_ok else "eager",
                        "published_us": w["published_fixed_us"],

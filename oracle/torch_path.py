@@ -1,5 +1,6 @@
-"""torch CPU restatement of one top-k decode-attention layer call (test infrastructure
-and the timed CPU baseline of ``bench.py``; never imported by ``interattn_amd``).
+"""torch CPU restatements of one decode-attention layer call, top-k and condition(eps)
+(test infrastructure and the timed CPU baselines of ``bench.py``; never imported by
+``interattn_amd``).
 
 The reference's CPU PyTorch path for a top-k step is the Quest convention
 (CBG/methods/quest.py:91-103: group-mean page score, ``torch.topk``, attention over
@@ -10,8 +11,14 @@ path on CPU tensors, one sequence at a time, reading K/V out of the paged pool
 through the block table (the gather is part of the work), so that ``bench.py`` can
 time it on the host cores next to the GPU path.
 
+The condition(eps) call restates the reference's own CPU path for its rule,
+``_select_prompt_blocks_eager`` (CBT/core.py:509-555) followed by
+``_condition_block_decode_output_dense`` (CBT/legacy.py:797-868), in float32 torch.
+
 Pinned against the numpy oracle (``oracle.select`` / ``oracle.attention``) by
-``tests/test_oracle.py::test_torch_path_matches_numpy_oracle``.
+``tests/test_oracle.py::test_torch_path_matches_numpy_oracle`` (top-k) and against
+the reference-written golden vectors and the numpy oracle by
+``tests/test_golden.py::test_torch_condition_path_matches_reference`` (condition).
 """
 
 import math
@@ -92,3 +99,76 @@ def topk_layer_call(q, pool_k, pool_v, table_row, seq_len, k_bar, *, block, page
         logits = torch.matmul(qf[h], kk.t()) / math.sqrt(d)
         out[h] = torch.matmul(torch.softmax(logits, dim=-1), vv)
     return out.view(hq, d), chosen_all
+
+
+# ------------------------------------------------------------- condition(eps) rule
+
+def condition_select(q_grouped, prefix, eps):
+    """The eager selection rule of ``_select_prompt_blocks_eager`` (CBT/core.py:509-555)
+    on CPU tensors in float32.  ``q_grouped [Hkv, G, 1, D]``; ``prefix`` holds
+    ``k_bar, k_max, k_min [Hkv, nb, D]``, ``v_norm_max [Hkv, nb]`` and
+    ``block_valid_counts [nb]``.  Returns ``(selected [Hkv, G, 1, nb] bool, z
+    [Hkv, G, 1, nb])``: per block s = q.k_bar/sqrt(D), the range bound delta from the
+    elementwise extrema, z = log(count) + s, p = softmax(z), and the condition
+    p (2 B_all (cosh delta - 1) / sum_b p cosh delta + 2 b_c tanh(delta/2)) averaged
+    over the group against eps."""
+    q = q_grouped.float()
+    hkv, g, nq, d = q.shape
+    inv = 1.0 / math.sqrt(d)
+    count = prefix["block_valid_counts"].long()
+    live = count > 0
+    s = torch.matmul(q, prefix["k_bar"].float().transpose(1, 2)[:, None]) * inv     # [hkv, g, nq, nb]
+    hi = q[..., None, :] * prefix["k_max"].float()[:, None, None]
+    lo = q[..., None, :] * prefix["k_min"].float()[:, None, None]
+    upper = torch.maximum(hi, lo).sum(-1) * inv
+    lower = torch.minimum(hi, lo).sum(-1) * inv
+    delta = torch.maximum((upper - s).abs(), (lower - s).abs()).masked_fill(~live, 0.0)
+    b_c = prefix["v_norm_max"].float()[:, None, None, :].masked_fill(~live, 0.0)
+    b_all = b_c.amax(-1, keepdim=True)
+    z = (s + count.clamp_min(1).float().log()).masked_fill(~live, float("-inf"))
+    p = torch.softmax(z, dim=-1)
+    ch = torch.cosh(delta)
+    mass = (p * ch).sum(-1, keepdim=True).clamp_min(1e-30)
+    cond = p * (2.0 * b_all * (ch - 1.0) / mass + 2.0 * b_c * torch.tanh(0.5 * delta))
+    chosen = (cond.mean(1, keepdim=True) > eps) & live
+    return chosen.expand(hkv, g, nq, -1), z
+
+
+def condition_attend(q_grouped, k_block, v_block, counts, z, selected, v_bar, k_suffix, v_suffix):
+    """The dense hybrid attention of ``_condition_block_decode_output_dense``
+    (CBT/legacy.py:797-868) on CPU tensors in float32, for a decode step that sees the
+    whole prompt and suffix: the selected blocks' valid tokens (``k_block, v_block
+    [Hkv, nb, B, D]``, the first ``counts[b]`` tokens of block b valid), one
+    representative per unselected non-empty block (logit z, value ``v_bar [Hkv, nb,
+    D]``) and the exact suffix ``[Hkv, S, D]``, one softmax over all of them.
+    Returns ``[Hkv, G, 1, D]``."""
+    q = q_grouped.float()[:, :, 0]                                                  # [hkv, g, d]
+    hkv, g, d = q.shape
+    nb, blk = k_block.shape[1], k_block.shape[2]
+    inv = 1.0 / math.sqrt(d)
+    live = counts.long() > 0
+    sel = selected[:, 0, 0] & live                                                  # [hkv, nb]
+    tok_ok = torch.arange(blk)[None, :] < counts.long()[:, None]                    # [nb, blk]
+    tok_logit = torch.matmul(q, k_block.float().reshape(hkv, nb * blk, d).transpose(1, 2)) * inv
+    tok_mask = (sel[:, :, None] & tok_ok[None]).reshape(hkv, 1, nb * blk)
+    tok_logit = tok_logit.masked_fill(~tok_mask, float("-inf"))
+    rep_logit = z.float()[:, :, 0].masked_fill(~((~sel) & live)[:, None, :], float("-inf"))
+    logits = [tok_logit, rep_logit]
+    values = [v_block.float().reshape(hkv, nb * blk, d), v_bar.float()]
+    if k_suffix.shape[1] > 0:
+        logits.append(torch.matmul(q, k_suffix.float().transpose(1, 2)) * inv)
+        values.append(v_suffix.float())
+    lg = torch.cat(logits, dim=-1)
+    top = lg.amax(-1, keepdim=True)
+    w = torch.exp(lg - torch.where(torch.isinf(top), torch.zeros_like(top), top))
+    num = torch.matmul(w, torch.cat(values, dim=1))
+    return (num / w.sum(-1, keepdim=True).clamp_min(1e-30))[:, :, None, :]
+
+
+def condition_layer_call(q_grouped, prefix, k_block, v_block, k_suffix, v_suffix, eps):
+    """One layer call of the reference's CPU path for its own rule: the eager selection
+    then the dense hybrid attention.  Returns ``(out [Hkv, G, 1, D], selected)``."""
+    selected, z = condition_select(q_grouped, prefix, eps)
+    out = condition_attend(q_grouped, k_block, v_block, prefix["block_valid_counts"], z, selected,
+                           prefix["v_bar"], k_suffix, v_suffix)
+    return out, selected

@@ -97,3 +97,43 @@ def test_hybrid_dense_output_matches_reference(path):
             fx["k_suffix"], fx["v_suffix"], fx[f"selected_{i}"], fx[f"z_{i}"], pre["v_bar"],
             pre["block_valid_counts"] > 0)
         np.testing.assert_allclose(out, fx[f"out_{i}"], rtol=1e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("path", FIXTURES, ids=[os.path.basename(p) for p in FIXTURES])
+def test_torch_condition_path_matches_reference(path):
+    """The timed torch CPU restatement of the reference's own CPU path for its rule
+    (oracle.torch_path.condition_layer_call: eager selection + dense hybrid attention)
+    against the reference-written selections and outputs, and against the numpy
+    oracle on the same inputs."""
+    import torch
+
+    from oracle import torch_path as T
+
+    fx = load(path)
+    hkv, g, d, b, p, s = (int(x) for x in fx["meta"])
+    pre = prefix_of(fx)
+    cm = condition_mean(fx["q"].astype(np.float64), pre, g)
+    tpre = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in pre.items()}
+    kb, vb = padded_blocks(fx["k"], b), padded_blocks(fx["v"], b)
+    nb = pre["block_valid_counts"].shape[0]
+    tok = np.arange(nb * b).reshape(nb, b)
+    for i, eps in enumerate(fx["eps"]):
+        out, sel = T.condition_layer_call(torch.from_numpy(fx["q"]), tpre, torch.from_numpy(kb),
+                                          torch.from_numpy(vb), torch.from_numpy(fx["k_suffix"]),
+                                          torch.from_numpy(fx["v_suffix"]), float(eps))
+        sel = sel.numpy()
+        diff = sel != fx[f"selected_{i}"]
+        if diff.any():
+            hh, _, _, jj = np.nonzero(diff)
+            assert np.all(np.abs(cm[hh, jj] - eps) <= 1e-5 * max(abs(eps), 1.0)), (i, eps)
+        # the output on the reference's own selection
+        _, z = T.condition_select(torch.from_numpy(fx["q"]), tpre, float(eps))
+        ref_sel = torch.from_numpy(fx[f"selected_{i}"])
+        got = T.condition_attend(torch.from_numpy(fx["q"]), torch.from_numpy(kb), torch.from_numpy(vb),
+                                 tpre["block_valid_counts"], z, ref_sel, tpre["v_bar"],
+                                 torch.from_numpy(fx["k_suffix"]), torch.from_numpy(fx["v_suffix"]))
+        np.testing.assert_allclose(got.numpy(), fx[f"out_{i}"], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(z.numpy(), fx[f"z_{i}"], rtol=1e-5, atol=1e-5)
+        ref = A.hybrid_decode_dense(fx["q"], kb, vb, tok < p, tok, p + s - 1, p, fx["k_suffix"], fx["v_suffix"],
+                                    sel, z.numpy(), pre["v_bar"], pre["block_valid_counts"] > 0)
+        np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=1e-5)

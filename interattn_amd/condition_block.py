@@ -11,8 +11,11 @@ and outputs live in the caller's ``workspace`` dict (``_workspace_empty``,
 CBT/core.py:558-570).
 """
 
+import contextlib
+import contextvars
 import math
 import os
+from collections import OrderedDict
 
 import torch
 import torch.nn.functional as F
@@ -21,6 +24,31 @@ from . import _native as N
 from .ops import _code, _require_cuda, _stream, workspace_tensor
 
 SELECT_CHUNK = 16  # blocks per selection-stats partial (CBT/core.py:27)
+
+# Whether the attention masks the dense decode hook receives allow a prefix [0, n) of
+# the keys (no left padding): set once per generation by the decode loops, which know
+# the prompt's mask, so the hook need not check every call (a device-to-host read).
+_MASK_PREFIX_HINT = contextvars.ContextVar("interattn_mask_prefix_hint", default=None)
+
+
+@contextlib.contextmanager
+def mask_prefix_hint(is_prefix):
+    """Inside the context the dense hook takes every attention mask to allow a prefix
+    of the keys (``True``) or not (``False``) without checking it."""
+    token = _MASK_PREFIX_HINT.set(bool(is_prefix))
+    try:
+        yield
+    finally:
+        _MASK_PREFIX_HINT.reset(token)
+
+
+def mask_is_prefix(attention_mask):
+    """Host decision for a 2-D ``[B, T]`` keep-mask (1 = attend): every row keeps a
+    prefix ``[0, n)`` of the positions.  Appending kept decode positions preserves it."""
+    m = attention_mask.to(torch.bool)
+    n = m.sum(-1, keepdim=True)
+    return bool(torch.equal(m, torch.arange(m.shape[-1], device=m.device)[None, :] < n))
+
 
 
 # ------------------------------------------------------------------ layout and summaries
@@ -330,6 +358,9 @@ def _condition_block_decode_output_fused_triton(*, q_grouped, prompt_prefix, k_s
                              store_selected, output_dtype, workspace)
 
 
+_SUFFIX_LEN_RECENT = 4  # uncaptured suffix-length tensors a fixed-mask workspace keeps
+
+
 def fixed_mask_hybrid_attention(*, q_grouped, prompt_prefix, selected, k_suffix, v_suffix, block_size,
                                 output_dtype, workspace=None):
     """Representative + selected-page attention with an external mask
@@ -352,12 +383,24 @@ def fixed_mask_hybrid_attention(*, q_grouped, prompt_prefix, selected, k_suffix,
                                 dtype=torch.uint8)
         mask.copy_(selected)
     # the suffix length lives in device memory: one tensor per length, written once, so
-    # a captured call and later calls of another length never share it
+    # a captured call and later calls of another length never share it.  Tensors that a
+    # captured graph reads are kept for the workspace's life; the others form a small
+    # least-recently-used set (an evicted tensor's memory is reused only by later work on
+    # the stream, after the calls that read it)
     s_len = int(k_suffix.shape[1]) if k_suffix is not None else 0
-    sfx_len = workspace.get(("suffix_len", s_len))
-    if sfx_len is None or sfx_len.device != q_grouped.device:
-        sfx_len = torch.full((1,), s_len, device=q_grouped.device, dtype=torch.int32)
-        workspace[("suffix_len", s_len)] = sfx_len
+    pinned = workspace.setdefault("suffix_len_captured", {})
+    recent = workspace.setdefault("suffix_len_recent", OrderedDict())
+    sfx_len = pinned.get(s_len)
+    if sfx_len is None:
+        sfx_len = recent.get(s_len)
+        if sfx_len is None or sfx_len.device != q_grouped.device:
+            sfx_len = torch.full((1,), s_len, device=q_grouped.device, dtype=torch.int32)
+            recent[s_len] = sfx_len
+        recent.move_to_end(s_len)
+        if torch.cuda.is_current_stream_capturing():
+            pinned[s_len] = recent.pop(s_len)
+        while len(recent) > _SUFFIX_LEN_RECENT:
+            recent.popitem(last=False)
     out, _ = _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, sfx_len, 0.0, False, False,
                                output_dtype, workspace, mask=mask)
     return out
@@ -435,11 +478,16 @@ def _sdpa_full_attention_forward(module, query, key, value, attention_mask, scal
         allowed = allowed.expand(bsz, t_len)
         seq = allowed.sum(-1).to(torch.int32).contiguous()
         # the kernel attends keys [0, n): a mask that is not such a prefix (left
-        # padding) goes to transformers' SDPA attention, as the reference's does
+        # padding) goes to transformers' SDPA attention, as the reference's does.  The
+        # decode loops say once per generation which kind their masks are
+        # (mask_prefix_hint); without that the mask is checked here (a host read)
         if torch.cuda.is_current_stream_capturing():
             raise ValueError("decode under graph capture takes attention_mask=None (keys [0, T) attended)")
-        prefix = torch.arange(t_len, device=allowed.device)[None, :] < seq[:, None]
-        if not bool(torch.equal(prefix, allowed)):
+        is_prefix = _MASK_PREFIX_HINT.get()
+        if is_prefix is None:
+            prefix = torch.arange(t_len, device=allowed.device)[None, :] < seq[:, None]
+            is_prefix = bool(torch.equal(prefix, allowed))
+        if not is_prefix:
             mask = attention_mask[..., :t_len] if attention_mask.dim() == 4 else attention_mask[:, None, :, :t_len]
             mask = mask if mask.dtype == torch.bool else mask.to(query.dtype)
             out = F.scaled_dot_product_attention(query, key, value, attn_mask=mask, scale=scaling,

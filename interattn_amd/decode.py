@@ -35,7 +35,8 @@ from types import SimpleNamespace
 import torch
 import torch.nn.functional as F
 
-from .condition_block import _build_prompt_blocks, _condition_block_decode_output, _sdpa_full_attention_forward
+from .condition_block import (_build_prompt_blocks, _condition_block_decode_output, _sdpa_full_attention_forward,
+                              mask_is_prefix, mask_prefix_hint)
 
 __all__ = [
     "ConditionBlockDecodeRunner",
@@ -506,7 +507,7 @@ def generate_condition_block_cached(*, model, tokenizer, input_ids, attention_ma
     step = _GreedyStep(model, runner, cache, first.view(1), prompt_len, n_new,
                        mask=torch.cat([attention_mask, torch.ones_like(first)], dim=1))
     n_done = 1
-    with condition_block_decode_context(runner), torch.no_grad():
+    with condition_block_decode_context(runner), mask_prefix_hint(mask_is_prefix(step.mask)), torch.no_grad():
         while n_done < n_new and not bool(torch.isin(step.tokens[n_done - 1], stop_ids)):
             runner.reset_step(prompt_len + n_done - 1)
             step()

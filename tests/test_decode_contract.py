@@ -59,3 +59,21 @@ def test_stats_helpers(monkeypatch):
     assert agg["rows"] == 128
     summ = decode.summarize_condition_block_step_metadata([decode._summarize_stats_lazy(agg, by)])
     assert summ["condition_block_equiv_budget"] == 1.0
+
+
+def test_mask_is_prefix_decision():
+    import torch
+
+    from interattn_amd.condition_block import _MASK_PREFIX_HINT, mask_is_prefix, mask_prefix_hint
+
+    assert mask_is_prefix(torch.ones((1, 7), dtype=torch.long))
+    assert mask_is_prefix(torch.tensor([[1, 1, 1, 0, 0], [1, 0, 0, 0, 0]]))
+    assert not mask_is_prefix(torch.tensor([[0, 0, 1, 1, 1]]))      # left padding
+    assert not mask_is_prefix(torch.tensor([[1, 0, 1, 1, 1]]))      # a hole
+    assert _MASK_PREFIX_HINT.get() is None
+    with mask_prefix_hint(False):
+        assert _MASK_PREFIX_HINT.get() is False
+        with mask_prefix_hint(True):
+            assert _MASK_PREFIX_HINT.get() is True
+        assert _MASK_PREFIX_HINT.get() is False
+    assert _MASK_PREFIX_HINT.get() is None

@@ -315,6 +315,40 @@ def test_fixed_mask_hybrid_vs_oracle(dt, device):
                                    err_msg=f"mask frac {frac}")
 
 
+def test_fixed_mask_suffix_length_tensors_are_bounded(device):
+    """One workspace over many suffix lengths keeps a few uncaptured suffix-length
+    tensors; one read by a captured graph stays, and every call is still right."""
+    c = ("sfxcache", 33, 2, 4, 128, 64, 3000, 9, "bf16", False, "f32", False)
+    name, seed, hkv, g, d, b, p, s, *_ = c
+    announce("fixed-mask: suffix-length tensors of one workspace")
+    host, dev = _make(c, device)
+    prefix = cb._build_prompt_blocks(dev["k"], dev["v"], b)
+    nb = int(prefix["block_valid_counts"].numel())
+    mask = torch.zeros((hkv, nb), dtype=torch.bool, device=device)
+    mask[:, ::3] = True
+    ws = {}
+
+    def call(n):
+        return cb.fixed_mask_hybrid_attention(q_grouped=dev["q"], prompt_prefix=prefix, selected=mask,
+                                              k_suffix=dev["ks"][:, :n], v_suffix=dev["vs"][:, :n], block_size=b,
+                                              output_dtype=torch.float32, workspace=ws)
+
+    refs = {}
+    for n in range(1, 10):
+        refs[n] = call(n).clone()
+        torch.cuda.synchronize()
+        assert len(ws["suffix_len_recent"]) <= 4
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call(2)
+    assert 2 in ws["suffix_len_captured"] and 2 not in ws["suffix_len_recent"]
+    for n in (5, 6, 7, 8, 9, 1, 3):  # churn the uncaptured set between replays
+        assert torch.equal(call(n), refs[n])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, refs[2])
+
+
 def test_fixed_mask_clustered_selection(device):
     """Clustered selections (all selected blocks contiguous inside one 256-block
     route chunk, a different chunk per kv head) are split over the finalize's items

@@ -3,11 +3,15 @@
 * the fused layer call equals select + decode bit for bit (indices and output);
 * the selected blocks equal the oracle's top-k of the same k_bar scores (near-tie
   rule) and the output equals exact attention over the selected tokens (float64,
-  2e-2 abs: bf16 weights): every sequence of C2 and C4, sampled sequences of C3;
+  2e-2 abs: bf16 weights): every sequence of C2, C3 and C4;
+* the device summaries of one full sequence of C4 (block 128) and of C3 (block 64)
+  equal the oracle's (counts, extrema exact; means within bf16 storage rounding);
 * C2: one 32768-token sequence, block 64, top-64 plus the first block and the last
   two (67 blocks), keys scaled per (kv head, channel) by exp(N(0,1));
+* C3: 16 ragged sequences whose pages are drawn from one shared pool of 4M tokens in
+  random order (BASELINE config 3);
 * C5: fp8 K/V against the oracle on the dequantised values (2e-3 + 2^-8 max|v|) on
-  two sequences, and within 6e-2 abs of the bf16 result on the same selection;
+  every sequence, and within 6e-2 abs of the bf16 result on the same selection;
 * the dense fallback over a whole 128K context equals float64 attention (2e-2).
 """
 
@@ -20,6 +24,7 @@ import torch
 import interattn_amd as ia
 from oracle import attention as A
 from oracle import select as S
+from oracle import summaries as Su
 from tests._util import announce, check_indices
 
 pytestmark = pytest.mark.gpu
@@ -27,11 +32,12 @@ pytestmark = pytest.mark.gpu
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
-def _make(device, lens, seed, k_outlier=False):
+def _make(device, lens, seed, k_outlier=False, pool_tokens=0):
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     pages = [math.ceil(L / PAGE) for L in lens]
-    n_pages = sum(pages)
+    # the sequences' pages come from one permutation of a pool of at least pool_tokens
+    n_pages = max(sum(pages), pool_tokens // PAGE)
     perm = torch.randperm(n_pages, device=device, generator=gen).to(torch.int32)
     table = torch.full((len(lens), max(pages)), -1, device=device, dtype=torch.int32)
     off = 0
@@ -60,6 +66,30 @@ def _gather_head(pool, table_row, blocks, block, L, h, scale=None):
     if scale is not None:
         x = x * scale[pg, h].double()[:, None]
     return x.cpu().numpy()
+
+
+def _check_summaries(pool_k, pool_v, table, seq, b, block, k_bar):
+    """The full summaries of sequence b (one build over its block-table row) against
+    the oracle's, per kv head; the k_bar that the top-k scored is the same array."""
+    L = int(seq[b])
+    nb = math.ceil(L / block)
+    got = ia.build_block_summaries(pool_k, pool_v, table[b:b + 1].contiguous(), seq[b:b + 1].contiguous(), block,
+                                   nb_max=nb, full=True, k_bar_dtype=torch.bfloat16, v_bar_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got["k_bar"][0], k_bar[b, :, :nb])
+    pg = table[b, :math.ceil(L / PAGE)].long()
+    for h in range(HKV):
+        kk = pool_k[pg, h].reshape(-1, D)[:L].float().cpu().numpy()[None]
+        vv = pool_v[pg, h].reshape(-1, D)[:L].float().cpu().numpy()[None]
+        ref = Su.build_block_summaries(kk, vv, block, k_bar_dtype="bf16", v_bar_dtype="bf16")
+        assert np.array_equal(got["block_valid_counts"][0, :nb].cpu().numpy(), ref["block_valid_counts"])
+        for key in ("k_bar", "v_bar"):
+            np.testing.assert_allclose(got[key][0, h:h + 1, :nb].float().cpu().numpy(), ref[key], rtol=2 ** -7,
+                                       atol=1e-5, err_msg=f"{key} head {h}")
+        for key in ("k_max", "k_min"):
+            assert np.array_equal(got[key][0, h:h + 1, :nb].float().cpu().numpy(), ref[key]), (key, h)
+        np.testing.assert_allclose(got["v_norm_max"][0, h:h + 1, :nb].cpu().numpy(), ref["v_norm_max"], rtol=1e-5)
+        np.testing.assert_allclose(got["v_norm_all"][0, h:h + 1].cpu().numpy(), ref["v_norm_all"], rtol=1e-5)
 
 
 def _check_sample(q, pool_k, pool_v, table, seq, k_bar, idx, n_sel, out, block, k, sample, k_per_seq=None,
@@ -108,8 +138,14 @@ def test_c4_fullsize(c4, device):
                   sample=range(16))
 
 
+def test_c4_fullsize_summaries(c4, device):
+    announce("C4 full size: summaries of sequence 5 against the oracle")
+    p = c4
+    _check_summaries(p["pool_k"], p["pool_v"], p["table"], p["seq"], 5, 128, p["k_bar"])
+
+
 def test_c5_fullsize_fp8(c4, device):
-    announce("C5 full size: fp8 K/V vs the oracle (two sequences) and vs bf16 on the same selection")
+    announce("C5 full size: fp8 K/V vs the oracle (every sequence) and vs bf16 on the same selection")
     p = c4
     pk, pv = p["pool_k"], p["pool_v"]
     ks = (pk.abs().amax(dim=(2, 3)).float().clamp_min(1e-12) / 448.0).contiguous()
@@ -127,7 +163,7 @@ def test_c5_fullsize_fp8(c4, device):
     err = (got.float() - ref.float()).abs().max().item()
     assert err <= 6e-2, err
     g = HQ // HKV
-    for b in (0, 9):
+    for b in range(16):
         L = int(p["seq"][b])
         qb = p["q"][b].double().cpu().numpy()
         for h in range(HKV):
@@ -159,9 +195,10 @@ def test_dense_fullsize_128k(c4, device):
 
 
 def test_c3_fullsize_ragged(device):
-    announce("C3 full size: ragged batch, k = max(16, nb/16)")
+    announce("C3 full size: ragged batch over a shared 4M-token pool, k = max(16, nb/16)")
     lens = [int(x) for x in np.random.default_rng(1236).integers(8192, 65537, size=16)]
-    pool_k, pool_v, table, seq, q = _make(device, lens, 1236)
+    pool_k, pool_v, table, seq, q = _make(device, lens, 1236, pool_tokens=4 << 20)
+    assert pool_k.shape[0] == (4 << 20) // PAGE
     nb_max = max(math.ceil(L / 64) for L in lens)
     summ = ia.build_block_summaries(pool_k, pool_v, table, seq, 64, nb_max=nb_max, k_bar_dtype=torch.bfloat16)
     kvec = torch.tensor([max(16, math.ceil(L / 64) // 16) for L in lens], device=device, dtype=torch.int32)
@@ -173,8 +210,11 @@ def test_c3_fullsize_ragged(device):
     torch.cuda.synchronize()
     assert torch.equal(n_sel, n_sel2) and torch.equal(out, out2)
     assert n_sel.cpu().tolist() == [[int(k)] * HKV for k in kvec.cpu().tolist()]
-    _check_sample(q, pool_k, pool_v, table, seq, summ["k_bar"], idx, n_sel, out, 64, 0, sample=(3, 11),
+    _check_sample(q, pool_k, pool_v, table, seq, summ["k_bar"], idx, n_sel, out, 64, 0, sample=range(16),
                   k_per_seq=kvec.cpu().numpy())
+    announce("C3 full size: summaries of the longest sequence against the oracle")
+    _check_summaries(pool_k, pool_v, table, seq, int(np.argmax(lens)), 64, summ["k_bar"])
+    del pool_k, pool_v
 
 
 def test_c2_fullsize(device):

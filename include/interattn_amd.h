@@ -309,6 +309,41 @@ IA_API int ia_condition_decode(const ia_decode_shape* shape, const void* q,
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ia_condition_decode in one launch.  Each (sequence, kv head) row is split into
+ * items that own equal runs of its blocks; an item computes the statistics of its
+ * blocks, the row's items exchange their partials of the row statistics (tagged
+ * words in the workspace, each wait bounded by the wait limit, a partial still
+ * missing then computed by the waiting item itself), every item merges them in
+ * item order, routes its blocks, forms the representative partial of its
+ * unselected blocks and streams its selected blocks (the last item also the exact
+ * suffix), and the last item of the row to finish merges the items' partials.
+ * The selection equals ia_condition_decode's except for blocks whose condition is
+ * within float rounding of eps (the row statistics are summed in another order);
+ * the output agrees to float rounding.  Arguments as for ia_condition_decode; the
+ * workspace (ia_condition_decode_fused_workspace_size bytes, sized by batch, heads,
+ * group and head_dim only) must be zero-filled before its first use and then left
+ * to the library: it carries per-row counts and epochs from call to call and may
+ * serve calls of any prompt length and eps with that (batch, n_kv_heads, group,
+ * head_dim).  Calls sharing a workspace must not overlap.  Returns
+ * IA_ERR_UNSUPPORTED when ia_condition_decode_fused_items is 0 for the call.
+ * Replaces _condition_block_decode_output_fused_triton (CBT/core.py:1035-1155).
+ */
+IA_API size_t ia_condition_decode_fused_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
+                                                       int32_t head_dim);
+/* Items per (sequence, kv head) of ia_condition_decode_fused on the current device
+ * for this call shape (kv_dtype IA_BF16 or IA_F32 matching q; suffix_cap as in
+ * ia_suffix_kv), or 0 when the call does not fit one launch: GQA groups above 4,
+ * head_dim other than 64 or 128, or more rows than the device holds items of at
+ * most 512 blocks at once.  No reference counterpart (a capability query). */
+IA_API int32_t ia_condition_decode_fused_items(const ia_decode_shape* shape, const ia_block_summaries* sm,
+                                               int32_t kv_dtype, int32_t suffix_cap);
+IA_API int ia_condition_decode_fused(const ia_decode_shape* shape, const void* q,
+                                     const ia_block_summaries* sm, const ia_paged_kv* prompt,
+                                     const ia_suffix_kv* suffix, float eps, int32_t term1_mass_exp,
+                                     uint8_t* selected, float scale, void* out, int32_t out_dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Hybrid decode with an external per-(batch, kv head) block mask [batch, Hkv, nb]
  * uint8: representatives recomputed as q.k_bar/sqrt(D) + log(count), q and k_bar
  * rounded to bfloat16 for bfloat16 caches.

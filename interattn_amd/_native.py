@@ -174,6 +174,13 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), ctypes.POINTER(PagedKV),
          ctypes.POINTER(SuffixKV), _F, _I32, _P, _F, _P, _I32, _P, _SZ, _P]),
+    "ia_condition_decode_fused_workspace_size": (_SZ, [_I32, _I32, _I32, _I32]),
+    "ia_condition_decode_fused_items": (
+        ctypes.c_int32, [ctypes.POINTER(DecodeShape), ctypes.POINTER(BlockSummaries), _I32, _I32]),
+    "ia_condition_decode_fused": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), ctypes.POINTER(PagedKV),
+         ctypes.POINTER(SuffixKV), _F, _I32, _P, _F, _P, _I32, _P, _SZ, _P]),
     "ia_fixed_mask_decode": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _P, ctypes.POINTER(PagedKV),

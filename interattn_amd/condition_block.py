@@ -21,7 +21,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _native as N
-from .ops import _code, _require_cuda, _stream, workspace_tensor
+from .ops import _code, _require_cuda, _scratch, _stream, workspace_tensor
 
 SELECT_CHUNK = 16  # blocks per selection-stats partial (CBT/core.py:27)
 
@@ -307,6 +307,13 @@ def _suffix_desc(k_suffix, v_suffix, suffix_len_dev, prompt_dtype):
     return sfx, [k_suffix, v_suffix, suffix_len_dev]
 
 
+def _one_launch():
+    """The condition rule's decode runs as one launch (``ia_condition_decode_fused``)
+    where the call fits one, unless ``INTERATTN_CONDITION_ONE_LAUNCH=0`` asks for the
+    four-launch path (statistics, route, finalize, merge)."""
+    return os.environ.get("INTERATTN_CONDITION_ONE_LAUNCH", "1") != "0"
+
+
 def _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, suffix_len_dev, eps, term1_mass_exp,
                       store_selected, output_dtype, workspace, mask=None):
     _require_cuda(q_grouped)
@@ -321,9 +328,12 @@ def _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, suffix_len_d
     sfx, keep_s = _suffix_desc(k_suffix, v_suffix, suffix_len_dev, k_block.dtype)
     dev = q.device
     lib = N.lib()
-    ws_bytes = lib.ia_condition_workspace_size(1, n_kv_heads, group_size, head_dim, nb, sfx.cap)
-    scratch = workspace_tensor(workspace, "condition_scratch", (max(int(ws_bytes), 1),), device=dev,
-                               dtype=torch.uint8)
+
+    def scratch():  # the four-launch and fixed-mask paths' workspace (no initialisation needed)
+        ws_bytes = lib.ia_condition_workspace_size(1, n_kv_heads, group_size, head_dim, nb, sfx.cap)
+        return workspace_tensor(workspace, "condition_scratch", (max(int(ws_bytes), 1),), device=dev,
+                                dtype=torch.uint8)
+
     out = workspace_tensor(workspace, "attention_output", (rows, head_dim), device=dev, dtype=output_dtype)
     if output_dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("output dtype must be float32 or bfloat16")
@@ -331,13 +341,24 @@ def _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, suffix_len_d
     if store_selected:
         selected = workspace_tensor(workspace, "selected_rows", (rows, nb), device=dev, dtype=torch.uint8)
     scale = head_dim ** -0.5
-    if mask is None:
+    if mask is None and _one_launch() and lib.ia_condition_decode_fused_items(sh, sm, kv.dtype, sfx.cap) > 0:
+        # one launch: its workspace carries per-row counts from call to call (zero-filled
+        # once, one per (heads, group, head_dim), whatever the prompt length and eps)
+        fws = _scratch(workspace, ("condition_fused_scratch", n_kv_heads, group_size, head_dim),
+                       lib.ia_condition_decode_fused_workspace_size(1, n_kv_heads, group_size, head_dim), dev)
+        rc = lib.ia_condition_decode_fused(sh, q.data_ptr(), sm, kv, sfx, float(eps), int(bool(term1_mass_exp)),
+                                           None if selected is None else selected.data_ptr(), scale,
+                                           out.data_ptr(), _code(output_dtype, "out"), fws.data_ptr(), fws.numel(),
+                                           _stream(q))
+    elif mask is None:
+        ws = scratch()
         rc = lib.ia_condition_decode(sh, q.data_ptr(), sm, kv, sfx, float(eps), int(bool(term1_mass_exp)),
                                      None if selected is None else selected.data_ptr(), scale, out.data_ptr(),
-                                     _code(output_dtype, "out"), scratch.data_ptr(), scratch.numel(), _stream(q))
+                                     _code(output_dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
     else:
+        ws = scratch()
         rc = lib.ia_fixed_mask_decode(sh, q.data_ptr(), sm, mask.data_ptr(), kv, sfx, scale, out.data_ptr(),
-                                      _code(output_dtype, "out"), scratch.data_ptr(), scratch.numel(), _stream(q))
+                                      _code(output_dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
     N.check(rc)
     del keep, keep_s
     out4 = out.reshape(n_kv_heads, group_size, 1, head_dim)

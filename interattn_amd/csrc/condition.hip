@@ -68,10 +68,6 @@ struct CondParams {
   int32_t rep_bf16;     // bfloat16 caches: representative operands rounded to bfloat16
 };
 
-__device__ __forceinline__ float round_if(float x, bool rnd) {
-  return rnd ? __uint_as_float((u32)f32_to_bf16_bits(x) << 16) : x;
-}
-
 // Raw words of one row slice of DPL elements (bf16 pairs or floats): loads are
 // issued before any use so a wave keeps all of its rows in flight at once.
 template <bool BF16, int DPL>
@@ -111,12 +107,6 @@ struct RawRow {
 __device__ __forceinline__ float q_elem(const CondParams& p, int64_t off) {
   return p.q_f32 ? reinterpret_cast<const float*>(p.q)[off]
                  : __uint_as_float((u32)reinterpret_cast<const unsigned short*>(p.q)[off] << 16);
-}
-
-// log cosh(d) = |d| + log(1 + e^{-2|d|}) - log 2, without overflow
-__device__ __forceinline__ float log_cosh(float d) {
-  const float a = fabsf(d);
-  return a + __logf(1.f + __expf(-2.f * a)) - 0.69314718055994531f;
 }
 
 // (m, l) <- log-sum-exp merge of (m, l) and (m2, l2); m = -inf marks an empty partial
@@ -325,30 +315,6 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_reduce(CondP
   }
 }
 
-// Condition of one (row, block): term1 + term2 with
-//   term1 = 2 B_all e^(z - c_m) (cosh(delta) - 1) / c_l   (mass_exp: 2 B_all e^(z + delta - c_m) / c_l)
-//   term2 = 2 b_c e^(z - z_m) tanh(delta / 2) / z_l
-// from one exponential of -delta (delta >= 0).  For delta >= 1/8
-// e^(z - c_m) (cosh(delta) - 1) = (1 - e^-delta)^2 e^(z - c_m + delta) / 2, which cannot
-// overflow before the product does; below it the Taylor series of cosh(delta) - 1 and
-// tanh(delta / 2) avoid the cancellation of 1 - e^-delta.  inv_zl = 1/z_l, inv_cl = 1/c_l.
-__device__ __forceinline__ float condition_value(float dl, float z, float zm, float inv_zl, float cm, float inv_cl,
-                                                 float b_c, float b_all, bool mass_exp) {
-  const float en = __expf(-dl);
-  float tanh_half, term1;
-  if (dl < 0.125f) {
-    const float d2 = dl * dl;
-    tanh_half = 0.5f * dl * (1.f - d2 * (1.f / 12.f) + d2 * d2 * (1.f / 120.f));
-    term1 = mass_exp ? 2.f * b_all * __expf(z + dl - cm) * inv_cl
-                     : b_all * __expf(z - cm) * d2 * (1.f + d2 * (1.f / 12.f) + d2 * d2 * (1.f / 360.f)) * inv_cl;
-  } else {
-    const float om = 1.f - en;
-    tanh_half = om / (1.f + en);
-    term1 = mass_exp ? 2.f * b_all * __expf(z + dl - cm) * inv_cl : b_all * om * om * __expf(z - cm + dl) * inv_cl;
-  }
-  return term1 + 2.f * b_c * __expf(z - zm) * tanh_half * inv_zl;
-}
-
 template <int G>
 __global__ __launch_bounds__(256) void ia_condition_block_selection_select(CondParams p) {
   const int j = blockIdx.x * 256 + threadIdx.x;
@@ -385,10 +351,6 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_select(CondP
 }
 
 // ---------------------------------------------------------------- route + representatives
-
-// Selected-block list entry for the finalize: block id in the low 16 bits, its
-// valid-token count above (block ids < 65536 and counts <= 32767 are host-checked).
-__device__ __forceinline__ int32_t list_entry(int j, int cnt) { return j | (cnt << 16); }
 
 template <int D, int G, bool VBH, bool KBH, bool MASK>
 __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
@@ -843,10 +805,176 @@ int run_condition(bool mask_mode, const ia_decode_shape* shape, const void* q, c
                          nullptr);
 }
 
+// ---------------------------------------------------------------- one-launch call
+
+// Workspace of the one-launch condition call, sized by (batch, Hkv, G, D) only so one
+// zero-filled buffer serves every prompt length and eps: the rows' lines (finished
+// items, epoch), the items' statistics partials [rows, kMaxItemsPerBh, 4 G] as tagged
+// words, and split-K partials for rows x kMaxItemsPerBh workgroup slots (untagged
+// (m, l) and accumulators, and tagged words for rows of at most 8 items).
+struct CondFusedWs {
+  size_t sbuf, part_ml, part_acc, tpart, total;
+};
+
+CondFusedWs cond_fused_ws_layout(int batch, int hkv, int g, int d) {
+  const size_t rows = (size_t)batch * hkv;
+  const size_t slots = rows * kMaxItemsPerBh;
+  CondFusedWs w{};
+  w.sbuf = align_up(rows * kFlagStride * 4, 256);
+  w.part_ml = align_up(w.sbuf + rows * kMaxItemsPerBh * 4 * g * 8, 256);
+  w.part_acc = align_up(w.part_ml + slots * g * 2 * 4, 256);
+  w.tpart = align_up(w.part_acc + slots * g * d * 4, 256);
+  w.total = align_up(w.tpart + slots * (g * d + 2 * g) * 8, 256);
+  return w;
+}
+
+// Items per (sequence, kv head) row of the one-launch call on the current device, or
+// 0 when the call does not fit one launch: every row's items must be resident at
+// once (they exchange their statistics), an item owns at most kCondItemBlocks
+// blocks and its selected blocks plus the suffix must fit the finalize's LDS lists.
+int cond_fused_items(int batch, int hkv, int g, int d, int nb, int block_size, int sfx_cap, int kv_dtype,
+                     bool q_f32, hipStream_t st) {
+  if (g > 4 || (d != 64 && d != 128) || nb <= 0 || nb > 65535 || batch <= 0) return 0;
+  if (kv_dtype != IA_BF16 && kv_dtype != IA_F32) return 0;
+  if ((kv_dtype == IA_F32) != q_f32) return 0;
+  DecodeParams probe{};
+  probe.q_f32 = q_f32;
+  int resident = 0;
+  if (dispatch_decode(probe, kv_dtype, d, g, kSrcCondFused, dim3(1), st, &resident) != IA_OK || resident <= 0)
+    return 0;
+  const int64_t rows = (int64_t)batch * hkv;
+  const int nsub_b = (block_size + 15) / 16;
+  const int sfx_sub = (std::max(sfx_cap, 0) + 15) / 16;
+  const int sfx_units = (std::max(sfx_cap, 0) + kDenseTile - 1) / kDenseTile;
+  const int m_cap = std::min({kCondItemBlocks, (kMaxSubsPerItem - sfx_sub) / std::max(nsub_b, 1),
+                              kMaxUnitsPerItem - sfx_units});
+  if (m_cap < 1) return 0;
+  const int64_t n_min = (nb + m_cap - 1) / m_cap;
+  // about one resident round, items of at least 16 blocks where the row allows
+  int64_t n = std::min<int64_t>({resident / rows, (int64_t)kMaxItemsPerBh, std::max<int64_t>(n_min, (nb + 15) / 16),
+                                 (int64_t)nb});
+  if (n < n_min || n < 1 || rows * n > resident) return 0;
+  return (int)n;
+}
+
+int run_condition_fused(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                        const ia_paged_kv* prompt, const ia_suffix_kv* sfx, float eps, int32_t mass_exp,
+                        uint8_t* selected, float scale, void* out, int32_t out_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  rc = check_summaries(sm, true, true);
+  if (rc) return rc;
+  rc = check_kv(prompt, shape->head_dim);
+  if (rc) return rc;
+  if (!q || !out) return fail(IA_ERR_INVALID, "q and out must be non-null");
+  if (out_dtype != IA_F32 && out_dtype != IA_BF16) return fail(IA_ERR_INVALID, "out dtype must be IA_F32 or IA_BF16");
+  if (!(scale > 0.f) || !std::isfinite(scale)) return fail(IA_ERR_INVALID, "scale must be positive and finite");
+  if (sfx && sfx->cap > 0) {
+    if (!sfx->k || !sfx->v || !sfx->len) return fail(IA_ERR_INVALID, "suffix needs k, v and a device length");
+    const int eb = prompt->dtype == IA_F32 ? 4 : 2;
+    const int64_t st6[6] = {sfx->k_batch_stride, sfx->k_head_stride, sfx->k_token_stride,
+                            sfx->v_batch_stride, sfx->v_head_stride, sfx->v_token_stride};
+    for (int64_t s6 : st6)
+      if (s6 < 0 || (s6 * eb) % 16) return fail(IA_ERR_INVALID, "suffix strides must be 16-byte multiples");
+    if ((reinterpret_cast<uintptr_t>(sfx->k) | reinterpret_cast<uintptr_t>(sfx->v)) % 16)
+      return fail(IA_ERR_INVALID, "suffix pointers must be 16-byte aligned");
+  }
+  const int G = shape->n_q_heads / shape->n_kv_heads;
+  const int D = shape->head_dim;
+  const int32_t sfx_cap = (sfx && sfx->cap > 0) ? sfx->cap : 0;
+  const CondFusedWs L = cond_fused_ws_layout(shape->batch, shape->n_kv_heads, G, D);
+  if (!workspace || workspace_bytes < L.total)
+    return fail(IA_ERR_WORKSPACE, "workspace too small: need " + std::to_string(L.total) + " bytes");
+  if (reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(IA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  if (shape->batch == 0) return IA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int n_it = cond_fused_items(shape->batch, shape->n_kv_heads, G, D, sm->nb, sm->block_size, sfx_cap,
+                                    prompt->dtype, shape->q_dtype == IA_F32, st);
+  if (n_it <= 0)
+    return fail(IA_ERR_UNSUPPORTED, "this condition call does not fit one launch; use ia_condition_decode");
+  char* ws = reinterpret_cast<char*>(workspace);
+
+  DecodeParams p{};
+  p.q = q;
+  p.q_batch_stride = shape->q_batch_stride;
+  p.q_row_stride = shape->q_row_stride;
+  p.kv = *prompt;
+  p.n_kv_heads = shape->n_kv_heads;
+  p.unit_tokens = sm->block_size;
+  p.scale_log2 = scale * kLog2e;
+  p.q_f32 = shape->q_dtype == IA_F32;
+  p.out_f32 = out_dtype == IA_F32;
+  p.out = out;
+  p.nb_max = sm->nb;
+  if (sfx_cap > 0) {
+    p.sfx_k = sfx->k;
+    p.sfx_v = sfx->v;
+    p.sfx_k_batch_stride = sfx->k_batch_stride;
+    p.sfx_k_head_stride = sfx->k_head_stride;
+    p.sfx_k_token_stride = sfx->k_token_stride;
+    p.sfx_v_batch_stride = sfx->v_batch_stride;
+    p.sfx_v_head_stride = sfx->v_head_stride;
+    p.sfx_v_token_stride = sfx->v_token_stride;
+    p.sfx_len = sfx->len;
+    p.sfx_len_stride = sfx->len_stride;
+    p.sfx_cap = sfx_cap;
+  }
+  p.n_rows = shape->batch * shape->n_kv_heads;
+  p.max_items = n_it;
+  p.rowctr = reinterpret_cast<u32*>(ws);
+  p.sbuf = reinterpret_cast<unsigned long long*>(ws + L.sbuf);
+  p.part_ml = reinterpret_cast<float*>(ws + L.part_ml);
+  p.part_acc = reinterpret_cast<float*>(ws + L.part_acc);
+  p.tpart = reinterpret_cast<unsigned long long*>(ws + L.tpart);
+  p.wait_ticks = wait_limit_ticks();
+  p.c_kbar = sm->k_bar;
+  p.c_kmax = sm->k_max;
+  p.c_kmin = sm->k_min;
+  p.c_vbar = sm->v_bar;
+  p.c_kbar_bf16 = sm->k_bar_dtype == IA_BF16;
+  p.c_bounds_bf16 = sm->bounds_dtype == IA_BF16;
+  p.c_vbar_bf16 = sm->v_bar_dtype == IA_BF16;
+  p.c_vnorm_max = sm->v_norm_max;
+  p.c_vnorm_all = sm->v_norm_all;
+  p.c_counts = sm->counts;
+  p.c_items = n_it;
+  p.c_eps = eps;
+  p.c_mass_exp = mass_exp;
+  p.c_scale = 1.0f / std::sqrt((float)D);
+  p.c_rep_bf16 = prompt->dtype == IA_BF16;
+  p.c_selected = selected;
+  return dispatch_decode(p, prompt->dtype, D, G, kSrcCondFused, dim3(p.n_rows * n_it), st, nullptr);
+}
+
 }  // namespace
 }  // namespace ia
 
 extern "C" {
+
+size_t ia_condition_decode_fused_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group,
+                                                int32_t head_dim) {
+  return ia::cond_fused_ws_layout(std::max(batch, 0), std::max(n_kv_heads, 0), std::max(group, 1),
+                                  std::max(head_dim, 1))
+      .total;
+}
+
+int32_t ia_condition_decode_fused_items(const ia_decode_shape* shape, const ia_block_summaries* sm,
+                                        int32_t kv_dtype, int32_t suffix_cap) {
+  if (ia::check_shape(shape) || !sm) return 0;
+  return ia::cond_fused_items(shape->batch, shape->n_kv_heads, shape->n_q_heads / shape->n_kv_heads,
+                              shape->head_dim, sm->nb, sm->block_size, suffix_cap, kv_dtype,
+                              shape->q_dtype == IA_F32, nullptr);
+}
+
+int ia_condition_decode_fused(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                              const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float eps,
+                              int32_t term1_mass_exp, uint8_t* selected, float scale, void* out, int32_t out_dtype,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  return ia::run_condition_fused(shape, q, sm, prompt, suffix, eps, term1_mass_exp, selected, scale, out, out_dtype,
+                                 workspace, workspace_bytes, stream);
+}
 
 size_t ia_condition_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim, int32_t nb,
                                    int32_t suffix_cap) {

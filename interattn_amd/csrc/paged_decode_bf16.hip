@@ -20,6 +20,13 @@ int run_bf16(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* res
     case kSrcTopkFused:
       if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcTopkFused>(), IA_OK;
       return launch_paged_finalize<D, G, KvBf16, kSrcTopkFused>(p, grid, st);
+    case kSrcCondFused:  // the one-launch condition call runs groups of up to 4 query rows
+      if constexpr (G <= 4) {
+        if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcCondFused>(), IA_OK;
+        return launch_paged_finalize<D, G, KvBf16, kSrcCondFused>(p, grid, st);
+      } else {
+        return fail(IA_ERR_UNSUPPORTED, "one-launch condition call: GQA group above 4");
+      }
   }
   return fail(IA_ERR_UNSUPPORTED, "unit source");
 }

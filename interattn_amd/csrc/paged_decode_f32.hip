@@ -20,6 +20,13 @@ int run_f32(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* resi
     case kSrcTopkFused:
       if (resident) return *resident = resident_wgs<D, G, KvF32, kSrcTopkFused>(), IA_OK;
       return launch_paged_finalize<D, G, KvF32, kSrcTopkFused>(p, grid, st);
+    case kSrcCondFused:  // the one-launch condition call runs groups of up to 4 query rows
+      if constexpr (G <= 4) {
+        if (resident) return *resident = resident_wgs<D, G, KvF32, kSrcCondFused>(), IA_OK;
+        return launch_paged_finalize<D, G, KvF32, kSrcCondFused>(p, grid, st);
+      } else {
+        return fail(IA_ERR_UNSUPPORTED, "one-launch condition call: GQA group above 4");
+      }
   }
   return fail(IA_ERR_UNSUPPORTED, "unit source");
 }

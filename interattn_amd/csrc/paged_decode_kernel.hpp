@@ -41,7 +41,9 @@
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
+#include "cond_rule.hpp"
 #include "plan.hpp"
 #include "topk_select.hpp"
 
@@ -86,7 +88,11 @@ constexpr int kSrcTopk = 0;   // idx[b, h, 0:n_sel[b, h]] blocks of unit_tokens 
 constexpr int kSrcDense = 1;  // every 128-token tile of [0, seq_len)
 constexpr int kSrcLists = 2;  // route-chunk lists of selected blocks, then the exact suffix
 constexpr int kSrcTopkFused = 3;  // top-k of a score row selected in the prologue, then as kSrcTopk
+constexpr int kSrcCondFused = 4;  // condition rule over the item's own blocks in the prologue, then as kSrcLists
 constexpr int kFusedMaxBlocks = 4096;  // score row staged in LDS by the fused top-k source
+constexpr int kCondItemBlocks = 512;   // blocks one item of the one-launch condition call owns at most
+// sources that merge their split-K partials inside the launch (the row's last item)
+constexpr bool src_fused(int src) { return src == kSrcTopkFused || src == kSrcCondFused; }
 
 constexpr int kRouteChunk = 256;      // blocks per route workgroup (condition mode)
 constexpr int kMaxRouteChunks = 256;  // route chunks per (sequence, kv head)
@@ -157,6 +163,27 @@ struct DecodeParams {
   unsigned long long* tpart; // [workgroups, G D + 2 G] tagged partials (acc, then (m, l)) of rows of <= 8 items
   u32* rowctr;               // [rows, kFlagStride]: finished partials (word 0), row epoch (word 1)
   int64_t wait_ticks;
+  // one-launch condition call (kSrcCondFused): the prompt blocks' summaries, rows of
+  // D elements at ((b * Hkv + h) * nb_max + j) * D (bf16 or fp32 each), their norm
+  // bounds [batch, Hkv, nb_max] and [batch, Hkv] and valid counts [batch, nb_max];
+  // the items per row; the rule's eps, variant (term1 mass exp) and 1/sqrt(D); the
+  // representatives' bf16 rounding (bf16 caches); the optional selected flags
+  // [batch, Hkv * G, nb_max].  The items' statistics partials travel through sbuf
+  // ([rows, kMaxItemsPerBh * 4 G] tagged words).
+  const void* c_kbar;
+  const void* c_kmax;
+  const void* c_kmin;
+  const void* c_vbar;
+  int32_t c_kbar_bf16, c_bounds_bf16, c_vbar_bf16;
+  const float* c_vnorm_max;
+  const float* c_vnorm_all;
+  const int32_t* c_counts;
+  int32_t c_items;
+  float c_eps;
+  int32_t c_mass_exp;
+  float c_scale;
+  int32_t c_rep_bf16;
+  uint8_t* c_selected;
 };
 
 constexpr int kWaves = 8;  // split-K merge: up to kWaves x kMergeFastSlots slots in one round trip
@@ -660,6 +687,12 @@ __device__ __forceinline__ void fused_merge_tagged(const DecodeParams& p, int b,
   }
 }
 
+}  // namespace ia
+
+#include "cond_fused.hpp"
+
+namespace ia {
+
 template <int D, int G, typename KV, int SRC>
 __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
@@ -693,14 +726,16 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ float wl_lds[kFinWaves][G];
 
   __shared__ PlanEntry plan_lds;
-  __shared__ u32 merge_todo[1];  // fused top-k call: this workgroup merges its row
+  __shared__ u32 merge_todo[1];  // fused calls: this workgroup merges its row
+  __shared__ std::conditional_t<SRC == kSrcCondFused, CondLds<D, G>, char> cond_lds;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c16 = lane & 15;
   const int r = lane >> 4;
   constexpr bool kBalanced = src_balanced(SRC);
-  const int nsub_u = ((SRC == kSrcLists ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
+  constexpr bool kListUnits = SRC == kSrcLists || SRC == kSrcCondFused;  // blocks then suffix tiles
+  const int nsub_u = ((kListUnits ? max(p.unit_tokens, kDenseTile) : p.unit_tokens) + 15) / 16;
   if (threadIdx.x < kFinWaves) wprog[threadIdx.x] = 0;  // read after the prologue's barriers
 
   // ---- this workgroup's (b, h) row and its item: from the launch plan (balanced
@@ -802,6 +837,15 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         e.seq_len = p.seq_lens[row_e / p.n_kv_heads];
         e.k_row = p.k_per_seq ? p.k_per_seq[row_e / p.n_kv_heads] : p.topk_k;
       }
+    } else if constexpr (SRC == kSrcCondFused) {
+      // every row alike: n items per row, consecutive plan slots (the items' units
+      // are known only after their routing)
+      const int n_it = p.c_items;
+      const int row = fused_slot / n_it;
+      e.row = row < p.n_rows ? row : -1;
+      e.item = fused_slot - row * n_it;
+      e.n_items = n_it;
+      e.slot_lo = e.slot_hi = e.n_units = e.seq_len = e.k_row = 0;
     } else {
       if (wave == 0) {
         PlanRows rows;
@@ -825,7 +869,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     if constexpr (SRC == kSrcTopkFused) {
       seq_len = max(__builtin_amdgcn_readfirstlane(e.seq_len), 0);
       k_b = max(__builtin_amdgcn_readfirstlane(e.k_row), 0);
-    } else {
+    } else if constexpr (SRC != kSrcCondFused) {
       seq_len = max(p.seq_lens[b], 0);
     }
   } else {
@@ -837,7 +881,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // (the epoch stays in a vector register until the publish, so its load is not
   // waited for here)
   u32 row_epoch_v = 0u;
-  if constexpr (SRC == kSrcTopkFused) row_epoch_v = ld_agent_u32(p.rowctr + (int64_t)bh * kFlagStride + 1);
+  if constexpr (src_fused(SRC)) row_epoch_v = ld_agent_u32(p.rowctr + (int64_t)bh * kFlagStride + 1);
   if constexpr (SRC != kSrcTopkFused) load_q(b, h);
 
   if constexpr (SRC == kSrcTopkFused) {
@@ -994,6 +1038,18 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     n_blk_units = rc_prefix[p.n_rc];
     sfx_len = p.sfx_len ? min(max(p.sfx_len[(int64_t)b * p.sfx_len_stride], 0), p.sfx_cap) : 0;
     n_units = n_blk_units + (sfx_len + kDenseTile - 1) / kDenseTile;
+  } else if constexpr (SRC == kSrcCondFused) {
+    // statistics, hand-off of the row's partials, routing and representatives of the
+    // item's own blocks; then its selected blocks and (last item) the suffix
+    row_epoch = __builtin_amdgcn_readfirstlane(row_epoch_v);
+    n_blk_units = __builtin_amdgcn_readfirstlane(
+        cond_fused_prologue<D, G>(p, cond_lds, b, h, item, n_items_row, row_epoch));
+    sfx_len = (item == n_items_row - 1 && p.sfx_len)
+                  ? min(max(p.sfx_len[(int64_t)b * p.sfx_len_stride], 0), p.sfx_cap)
+                  : 0;
+    n_units = n_blk_units + (sfx_len + kDenseTile - 1) / kDenseTile;
+    slot_lo = 0;
+    slot_hi = n_units * nsub_u;
   }
   bool split;
   int u_begin, nu;
@@ -1054,6 +1110,16 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     } else if constexpr (SRC == kSrcDense) {
       lo = u * p.unit_tokens;
       hi = min(lo + p.unit_tokens, seq_len);
+    } else if constexpr (SRC == kSrcCondFused) {
+      if (u < n_blk_units) {  // entry = block id | valid tokens << 16
+        const int e = cond_lds.list[u];
+        lo = (e & 0xffff) * p.unit_tokens;
+        hi = lo + max(0, min(e >> 16, p.unit_tokens));
+      } else {
+        lo = (u - n_blk_units) * kDenseTile;
+        hi = min(lo + kDenseTile, sfx_len);
+        sfx = 1;
+      }
     } else {
       if (u < n_blk_units) {
         int lo_c = 0, hi_c = p.n_rc - 1;  // last chunk whose prefix <= u
@@ -1159,7 +1225,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
 
   // K and V row pointers of a subtile and their row strides in bytes
   auto sub_rows = [&](const Sub& sb, const char*& kp, const char*& vp, int64_t& kts, int64_t& vts) {
-    if (SRC == kSrcLists && sb.pg == kSfxPage) {
+    if (kListUnits && sb.pg == kSfxPage) {
       kts = p.sfx_k_token_stride * KV::kBytes;
       vts = p.sfx_v_token_stride * KV::kBytes;
       kp = reinterpret_cast<const char*>(p.sfx_k) +
@@ -1607,12 +1673,13 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // last item to finish merges them)
   // a fused call's item keeps its partial in its workgroup's slot (the row's items
   // are consecutive workgroups), others at (row, item)
-  const int64_t pbase = SRC == kSrcTopkFused ? (int64_t)fused_slot : (int64_t)bh * p.max_items + item;
+  const int64_t pbase = src_fused(SRC) ? (int64_t)fused_slot : (int64_t)bh * p.max_items + item;
   for (int o = threadIdx.x; o < G * D; o += kFinThreads) {
     const int g = o / D;
     float M = kNegInf;
 #pragma unroll
     for (int w = 0; w < kFinWaves; ++w) M = fmaxf(M, wm_lds[w][g]);
+    if constexpr (SRC == kSrcCondFused) M = fmaxf(M, cond_lds.rep_m[g]);
     float a = 0.f, l = 0.f;
     if (M != kNegInf) {
 #pragma unroll
@@ -1622,10 +1689,21 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         a += f * wacc_lds[w][o];
         l += f * wl_lds[w][g];
       }
+      if constexpr (SRC == kSrcCondFused) {  // the representatives of the item's blocks
+        const float mr = cond_lds.rep_m[g];
+        if (mr != kNegInf) {
+          float ra = 0.f;
+#pragma unroll
+          for (int w = 0; w < kFinWaves; ++w) ra += cond_lds.rep_acc[w][o];
+          const float f = exp2f(mr - M);
+          a += f * ra;
+          l += f * cond_lds.rep_l[g];
+        }
+      }
     }
     if (!split) {
       store_decode_out<G, D>(p, b, h, o, a / fmaxf(l, 1e-30f));
-    } else if (SRC == kSrcTopkFused && n_items_row <= kMergeGroup) {
+    } else if (src_fused(SRC) && n_items_row <= kMergeGroup) {
       // tagged words: readable as soon as they land, no acknowledgement to wait for
       const unsigned long long tg = (unsigned long long)partial_tag(bh, row_epoch) << 32;
       unsigned long long* slot = p.tpart + pbase * (G * D + 2 * G);
@@ -1634,7 +1712,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         st_agent_u64(slot + G * D + 2 * g, tg | __float_as_uint(M));
         st_agent_u64(slot + G * D + 2 * g + 1, tg | __float_as_uint(l));
       }
-    } else if (SRC == kSrcTopkFused) {
+    } else if (src_fused(SRC)) {
       st_agent(p.part_acc + pbase * (G * D) + o, a);
       if (o % D == 0) {
         st_agent(p.part_ml + (pbase * G + g) * 2 + 0, M);
@@ -1648,7 +1726,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     }
   }
-  if constexpr (SRC == kSrcTopkFused) {
+  if constexpr (src_fused(SRC)) {
     if (split) {
       // the row's items count their finished partials; the one that brings the count
       // to n merges and resets the count for the next call.  Untagged partials (rows
@@ -1949,8 +2027,8 @@ template <int D, int G, typename KV, int SRC>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
   hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kFinThreads), 0, st, p);
   int rc = check_launch("paged decode");
-  if constexpr (SRC == kSrcTopkFused) {
-    return rc;  // item 0 of each row merges inside the launch
+  if constexpr (src_fused(SRC)) {
+    return rc;  // the row's last item merges inside the launch
   } else if constexpr (src_balanced(SRC)) {
     // a flat grid of at most n_rows workgroups gives every row a single item
     if (rc || (int)grid.x <= p.n_rows) return rc;

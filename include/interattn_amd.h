@@ -344,6 +344,21 @@ IA_API int ia_condition_decode_fused(const ia_decode_shape* shape, const void* q
                                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ia_fixed_mask_decode in one launch: the one-launch call of
+ * ia_condition_decode_fused with the caller's mask as the selection (no statistics,
+ * no hand-off between the items); each item's representatives are weighted against
+ * their own largest logit.  The output agrees with ia_fixed_mask_decode's to float
+ * rounding.  Workspace and fit as for ia_condition_decode_fused (k_max and k_min are
+ * not read).  Replaces fixed_mask_hybrid_attention
+ * (CBG/real_attention_benchmark/fixed_mask.py:250-348).
+ */
+IA_API int ia_fixed_mask_decode_fused(const ia_decode_shape* shape, const void* q,
+                                      const ia_block_summaries* sm, const uint8_t* mask,
+                                      const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float scale,
+                                      void* out, int32_t out_dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
+/*
  * Hybrid decode with an external per-(batch, kv head) block mask [batch, Hkv, nb]
  * uint8: representatives recomputed as q.k_bar/sqrt(D) + log(count), q and k_bar
  * rounded to bfloat16 for bfloat16 caches.

@@ -181,6 +181,10 @@ SIGNATURES = {
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), ctypes.POINTER(PagedKV),
          ctypes.POINTER(SuffixKV), _F, _I32, _P, _F, _P, _I32, _P, _SZ, _P]),
+    "ia_fixed_mask_decode_fused": (
+        ctypes.c_int,
+        [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _P, ctypes.POINTER(PagedKV),
+         ctypes.POINTER(SuffixKV), _F, _P, _I32, _P, _SZ, _P]),
     "ia_fixed_mask_decode": (
         ctypes.c_int,
         [ctypes.POINTER(DecodeShape), _P, ctypes.POINTER(BlockSummaries), _P, ctypes.POINTER(PagedKV),

@@ -308,9 +308,10 @@ def _suffix_desc(k_suffix, v_suffix, suffix_len_dev, prompt_dtype):
 
 
 def _one_launch():
-    """The condition rule's decode runs as one launch (``ia_condition_decode_fused``)
-    where the call fits one, unless ``INTERATTN_CONDITION_ONE_LAUNCH=0`` asks for the
-    four-launch path (statistics, route, finalize, merge)."""
+    """The condition rule's decode (``ia_condition_decode_fused``) and the fixed-mask
+    decode (``ia_fixed_mask_decode_fused``) run as one launch where the call fits one,
+    unless ``INTERATTN_CONDITION_ONE_LAUNCH=0`` asks for the multi-launch paths
+    (statistics, route, finalize, merge; route, finalize, merge)."""
     return os.environ.get("INTERATTN_CONDITION_ONE_LAUNCH", "1") != "0"
 
 
@@ -355,6 +356,11 @@ def _condition_decode(q_grouped, prompt_prefix, k_suffix, v_suffix, suffix_len_d
         rc = lib.ia_condition_decode(sh, q.data_ptr(), sm, kv, sfx, float(eps), int(bool(term1_mass_exp)),
                                      None if selected is None else selected.data_ptr(), scale, out.data_ptr(),
                                      _code(output_dtype, "out"), ws.data_ptr(), ws.numel(), _stream(q))
+    elif _one_launch() and lib.ia_condition_decode_fused_items(sh, sm, kv.dtype, sfx.cap) > 0:
+        fws = _scratch(workspace, ("condition_fused_scratch", n_kv_heads, group_size, head_dim),
+                       lib.ia_condition_decode_fused_workspace_size(1, n_kv_heads, group_size, head_dim), dev)
+        rc = lib.ia_fixed_mask_decode_fused(sh, q.data_ptr(), sm, mask.data_ptr(), kv, sfx, scale, out.data_ptr(),
+                                            _code(output_dtype, "out"), fws.data_ptr(), fws.numel(), _stream(q))
     else:
         ws = scratch()
         rc = lib.ia_fixed_mask_decode(sh, q.data_ptr(), sm, mask.data_ptr(), kv, sfx, scale, out.data_ptr(),

@@ -51,22 +51,29 @@ constexpr bool cond_vbar_early() { return G <= 4; }
 // First block of item i of n over a row of nb blocks.
 __device__ __forceinline__ int cond_range_lo(int i, int nb, int n) { return (int)(((int64_t)i * nb) / n); }
 
-// Values per lane of the statistics' row reduce-scatter: s, A and B for G query rows,
-// padded to a power of two.
-template <int G>
-constexpr int cond_nv() { return 3 * G <= 4 ? 4 : 3 * G <= 8 ? 8 : 3 * G <= 16 ? 16 : 32; }
+// Values per lane of the statistics' row reduce-scatter: s, A and B for G query rows
+// (external-mask mode: s only), padded to a power of two.
+template <int G, bool MASK>
+constexpr int cond_nv() {
+  return (MASK ? G : 3 * G) <= 4 ? 4 : (MASK ? G : 3 * G) <= 8 ? 8 : (MASK ? G : 3 * G) <= 16 ? 16 : 32;
+}
 
 // Steps 1-3 for item `item` of the n_it items of row (b, h).  SBF: the k_bar, bound
 // and v_bar rows are all bf16 (one load per row slice); else their dtypes are read
-// at run time.  Returns the number of selected blocks in the item's range (their
+// at run time.  MASK: the external-mask mode of fixed_mask_hybrid_attention
+// (CBG/real_attention_benchmark/fixed_mask.py:38-239): the selection is the caller's
+// mask [batch, Hkv, nb], there are no statistics to exchange, and a representative's
+// logit is bf16(q) . bf16(k_bar) / sqrt(D) + log(count) for bf16 caches (q . k_bar /
+// sqrt(D) + log(count) for fp32 caches), weighted against the largest of the item's
+// representative logits.  Returns the number of selected blocks in the item's range (their
 // list entries in L.list); the representative partial is left in L.rep_acc (one
 // accumulator per wave, summed by the finalize's fold) / rep_m / rep_l.  Every
 // thread of the workgroup calls it.
-template <int D, int G, int SBF>
+template <int D, int G, int SBF, bool MASK>
 __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, CondLds<D, G>& L, int b, int h, int item,
                                                      int n_it, u32 row_epoch) {
   constexpr int DPL = D / 16;
-  constexpr int NV = cond_nv<G>();
+  constexpr int NV = cond_nv<G, MASK>();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c16 = lane & 15;
@@ -95,8 +102,9 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   const bool mine = t < m;
   const int jt = lo + min(t, m - 1);
   const int cnt_ld = p.c_counts[(int64_t)b * nb + jt];
-  const float bc_ld = p.c_vnorm_max[vrow + jt];
-  const float b_all = p.c_vnorm_all[bh];
+  const float bc_ld = MASK ? 0.f : p.c_vnorm_max[vrow + jt];
+  const float b_all = MASK ? 0.f : p.c_vnorm_all[bh];
+  const bool mask_ld = MASK && p.c_mask[vrow + jt] != 0;
   SumRow<DPL, SBF> vpre[kEarlyV ? 2 : 1];
   if constexpr (kEarlyV) {
 #pragma unroll
@@ -115,20 +123,23 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     const int nsteps = (rm + 31) / 32;
     const int cl = t < rm ? p.c_counts[(int64_t)b * nb + rlo + t] : 0;
     for (int s0 = 0; s0 < nsteps; s0 += kSteps) {
-      SumRow<DPL, SBF> kb[kSteps], kx[kSteps], kn[kSteps];
+      SumRow<DPL, SBF> kb[kSteps], kx[MASK ? 1 : kSteps], kn[MASK ? 1 : kSteps];
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {
         const int64_t off = (vrow + rlo + min(32 * (s0 + u) + 4 * wave + r, rm - 1)) * D + c16 * DPL;
         kb[u].load(p.c_kbar, off, kbf);
-        kx[u].load(p.c_kmax, off, xbf);
-        kn[u].load(p.c_kmin, off, xbf);
+        if constexpr (!MASK) {
+          kx[u].load(p.c_kmax, off, xbf);
+          kn[u].load(p.c_kmin, off, xbf);
+        }
       }
       if (s0 == 0 && t < kCondItemBlocks) L.lc[t] = cl > 0 ? __logf((float)cl) : kNegInf;
+      // (external mask: bf16(q) and bf16(k_bar) for bf16 caches, fixed_mask.py:86-107)
       float qf[G][DPL];
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) qf[g][e] = qw[g].at(e, qbf);
+        for (int e = 0; e < DPL; ++e) qf[g][e] = MASK ? round_if(qw[g].at(e, qbf), p.c_rep_bf16) : qw[g].at(e, qbf);
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {
         if (s0 + u >= nsteps) break;
@@ -136,10 +147,15 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
         float ksum[DPL], kdif[DPL], kbv[DPL];
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
-          const float hx = kx[u].at(e, xbf), ln = kn[u].at(e, xbf);
-          ksum[e] = hx + ln;
-          kdif[e] = hx - ln;
-          kbv[e] = kb[u].at(e, kbf);
+          if constexpr (MASK) {
+            kbv[e] = round_if(kb[u].at(e, kbf), p.c_rep_bf16 && !kbf);
+            ksum[e] = kdif[e] = 0.f;
+          } else {
+            const float hx = kx[u].at(e, xbf), ln = kn[u].at(e, xbf);
+            ksum[e] = hx + ln;
+            kdif[e] = hx - ln;
+            kbv[e] = kb[u].at(e, kbf);
+          }
         }
         float v[NV];
 #pragma unroll
@@ -151,12 +167,16 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
           for (int e = 0; e < DPL; ++e) {
             const float qv = qf[g][e];
             a = fmaf(qv, kbv[e], a);
-            sa = fmaf(qv, ksum[e], sa);
-            sb = fmaf(fabsf(qv), kdif[e], sb);
+            if constexpr (!MASK) {
+              sa = fmaf(qv, ksum[e], sa);
+              sb = fmaf(fabsf(qv), kdif[e], sb);
+            }
           }
           v[g] = a;
-          v[G + g] = sa;
-          v[2 * G + g] = sb;
+          if constexpr (!MASK) {
+            v[G + g] = sa;
+            v[2 * G + g] = sb;
+          }
         }
         reduce_scatter16<NV>(v, lane);
         // value index x sits in lane src(x) of the row, in v[0] (v[x & 1] for NV = 32)
@@ -171,11 +191,15 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
         };
         const int gq = c16 < G ? c16 : 0;
         const float sv = fetch(gq) * p.c_scale;
-        const float av = fetch(G + gq), bv = fetch(2 * G + gq);
-        const float dl = fabsf(0.5f * av * p.c_scale - sv) + 0.5f * bv * p.c_scale;
-        if (c16 < G && jl < rm) {
-          L.s[c16][jl] = sv;
-          L.dl[c16][jl] = dl;
+        if constexpr (MASK) {
+          if (c16 < G && jl < rm) L.s[c16][jl] = sv;
+        } else {
+          const float av = fetch(G + gq), bv = fetch(2 * G + gq);
+          const float dl = fabsf(0.5f * av * p.c_scale - sv) + 0.5f * bv * p.c_scale;
+          if (c16 < G && jl < rm) {
+            L.s[c16][jl] = sv;
+            L.dl[c16][jl] = dl;
+          }
         }
       }
     }
@@ -217,8 +241,9 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
 
   stats_range(lo, hi);
   __syncthreads();
-  range_partial(m);
-  if (n_it > 1) {  // (a row of one item hands nothing over: every published word
+  if constexpr (!MASK) range_partial(m);
+  if (MASK) {
+  } else if (n_it > 1) {  // (a row of one item hands nothing over: every published word
                    // belongs to a call that advances the row's epoch)
     // ---- step 2: the own partial as tagged words, then the other items'
     const u32 tag = partial_tag(bh, row_epoch);
@@ -261,11 +286,11 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   } else if (t < 4 * G) {
     L.part[0][t / G][t % G] = L.own[t / G][t % G];
   }
-  __syncthreads();
+  if constexpr (!MASK) __syncthreads();
 
   // ---- step 3: the row's globals, the items' partials merged in item order (wave w
   // takes (value, row) pairs w, w + 8, ...: lanes are items)
-  for (int pr = wave; pr < 2 * G; pr += kFinWaves) {
+  for (int pr = wave; !MASK && pr < 2 * G; pr += kFinWaves) {
     const int v = pr / G, g = pr - v * G;
     const float mi = lane < n_it ? L.part[lane][2 * v][g] : kNegInf;
     const float li = lane < n_it ? L.part[lane][2 * v + 1][g] : 0.f;
@@ -276,9 +301,10 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
       L.glob[2 * v + 1][g] = S;
     }
   }
-  __syncthreads();
+  if constexpr (!MASK) __syncthreads();
 
-  // routing of this thread's block: the group mean of the condition against eps
+  // routing of this thread's block: the group mean of the condition against eps (or
+  // the caller's mask)
   const int cnt = mine ? cnt_ld : 0;  // this thread's block's valid tokens (0: none)
   const float b_c = mine ? bc_ld : 0.f;
   const bool act = cnt > 0;
@@ -288,13 +314,30 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     zr[g] = act ? L.s[g][t] + logc : kNegInf;
-    if (act)
+    if (!MASK && act)
       mean += condition_value(L.dl[g][t], zr[g], L.glob[0][g], 1.f / L.glob[1][g], L.glob[2][g], 1.f / L.glob[3][g],
                               b_c, b_all, p.c_mass_exp);
   }
   mean /= (float)G;
-  const bool sel = act && mean > p.c_eps;
-  if (p.c_selected && mine) {
+  const bool sel = act && (MASK ? mask_ld : mean > p.c_eps);
+  // external mask: the representatives' own largest logit per query row (no row
+  // globals): the waves' maxima through LDS
+  if constexpr (MASK) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mx = wave_max(sel ? kNegInf : zr[g]);
+      if (lane == 0) L.part[wave][0][g] = mx;
+    }
+    __syncthreads();
+    if (t < G) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int w = 0; w < kFinWaves; ++w) mx = fmaxf(mx, L.part[w][0][t]);
+      L.glob[0][t] = mx;
+    }
+    __syncthreads();
+  }
+  if (!MASK && p.c_selected && mine) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
       p.c_selected[((int64_t)b * p.n_kv_heads * G + h * G + g) * nb + lo + t] = sel ? 1 : 0;
@@ -372,9 +415,13 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
 template <int D, int G>
 __device__ __forceinline__ int cond_fused_prologue(const DecodeParams& p, CondLds<D, G>& L, int b, int h, int item,
                                                    int n_it, u32 row_epoch) {
+  if (p.c_mask) {
+    if (p.c_kbar_bf16 && p.c_vbar_bf16) return cond_fused_prologue_t<D, G, 1, true>(p, L, b, h, item, n_it, row_epoch);
+    return cond_fused_prologue_t<D, G, 0, true>(p, L, b, h, item, n_it, row_epoch);
+  }
   if (p.c_kbar_bf16 && p.c_bounds_bf16 && p.c_vbar_bf16)
-    return cond_fused_prologue_t<D, G, 1>(p, L, b, h, item, n_it, row_epoch);
-  return cond_fused_prologue_t<D, G, 0>(p, L, b, h, item, n_it, row_epoch);
+    return cond_fused_prologue_t<D, G, 1, false>(p, L, b, h, item, n_it, row_epoch);
+  return cond_fused_prologue_t<D, G, 0, false>(p, L, b, h, item, n_it, row_epoch);
 }
 
 }  // namespace ia

@@ -857,13 +857,13 @@ int cond_fused_items(int batch, int hkv, int g, int d, int nb, int block_size, i
   return (int)n;
 }
 
-int run_condition_fused(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
-                        const ia_paged_kv* prompt, const ia_suffix_kv* sfx, float eps, int32_t mass_exp,
-                        uint8_t* selected, float scale, void* out, int32_t out_dtype, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+int run_condition_fused(const uint8_t* mask, const ia_decode_shape* shape, const void* q,
+                        const ia_block_summaries* sm, const ia_paged_kv* prompt, const ia_suffix_kv* sfx, float eps,
+                        int32_t mass_exp, uint8_t* selected, float scale, void* out, int32_t out_dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_shape(shape);
   if (rc) return rc;
-  rc = check_summaries(sm, true, true);
+  rc = check_summaries(sm, !mask, true);
   if (rc) return rc;
   rc = check_kv(prompt, shape->head_dim);
   if (rc) return rc;
@@ -944,7 +944,8 @@ int run_condition_fused(const ia_decode_shape* shape, const void* q, const ia_bl
   p.c_mass_exp = mass_exp;
   p.c_scale = 1.0f / std::sqrt((float)D);
   p.c_rep_bf16 = prompt->dtype == IA_BF16;
-  p.c_selected = selected;
+  p.c_selected = mask ? nullptr : selected;
+  p.c_mask = mask;
   return dispatch_decode(p, prompt->dtype, D, G, kSrcCondFused, dim3(p.n_rows * n_it), st, nullptr);
 }
 
@@ -972,7 +973,16 @@ int ia_condition_decode_fused(const ia_decode_shape* shape, const void* q, const
                               const ia_paged_kv* prompt, const ia_suffix_kv* suffix, float eps,
                               int32_t term1_mass_exp, uint8_t* selected, float scale, void* out, int32_t out_dtype,
                               void* workspace, size_t workspace_bytes, void* stream) {
-  return ia::run_condition_fused(shape, q, sm, prompt, suffix, eps, term1_mass_exp, selected, scale, out, out_dtype,
+  return ia::run_condition_fused(nullptr, shape, q, sm, prompt, suffix, eps, term1_mass_exp, selected, scale, out,
+                                 out_dtype, workspace, workspace_bytes, stream);
+}
+
+int ia_fixed_mask_decode_fused(const ia_decode_shape* shape, const void* q, const ia_block_summaries* sm,
+                               const uint8_t* mask, const ia_paged_kv* prompt, const ia_suffix_kv* suffix,
+                               float scale, void* out, int32_t out_dtype, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  if (!mask) return ia::fail(IA_ERR_INVALID, "fixed-mask decode needs a mask");
+  return ia::run_condition_fused(mask, shape, q, sm, prompt, suffix, 0.f, 0, nullptr, scale, out, out_dtype,
                                  workspace, workspace_bytes, stream);
 }
 

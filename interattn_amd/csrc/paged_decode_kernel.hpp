@@ -184,6 +184,7 @@ struct DecodeParams {
   float c_scale;
   int32_t c_rep_bf16;
   uint8_t* c_selected;
+  const uint8_t* c_mask;  // external-mask mode: the selection [batch, Hkv, nb_max] (no statistics)
 };
 
 constexpr int kWaves = 8;  // split-K merge: up to kWaves x kMergeFastSlots slots in one round trip

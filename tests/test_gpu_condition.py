@@ -8,9 +8,10 @@ condition lies within 1e-3 relative (plus 1e-5 absolute) of eps; outputs within
 ``_condition_block_decode_output_dense`` (CBT/legacy.py:797-868) evaluated on the
 GPU's own selection; statistics and routing counts exact.
 
-The decode tests run both implementations of the fused entry point: the one-launch
-call (``ia_condition_decode_fused``, the default where a call fits one launch) and
-the four-launch path (statistics, route, finalize, merge).
+The decode tests run both implementations of the fused and fixed-mask entry points:
+the one-launch calls (``ia_condition_decode_fused``, ``ia_fixed_mask_decode_fused``,
+the default where a call fits one launch) and the multi-launch paths (statistics,
+route, finalize, merge; route, finalize, merge).
 """
 
 import glob
@@ -309,10 +310,10 @@ def test_condition_decode_ignores_workspace_contents(case, device, monkeypatch):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
-def test_fixed_mask_hybrid_vs_oracle(dt, device):
+def test_fixed_mask_hybrid_vs_oracle(dt, path, device):
     c = ("mask", 31, 4, 4, 128, 64, 10000, 7, dt, False, "f32", False)
     name, seed, hkv, g, d, b, p, s, *_ = c
-    announce(f"fixed-mask {dt}")
+    announce(f"fixed-mask {dt} ({path})")
     host, dev = _make(c, device)
     prefix = cb._build_prompt_blocks(dev["k"], dev["v"], b)
     pre = _prefix_np(prefix)
@@ -365,14 +366,14 @@ def test_fixed_mask_suffix_length_tensors_are_bounded(device):
         assert torch.equal(out, refs[2])
 
 
-def test_fixed_mask_clustered_selection(device):
+def test_fixed_mask_clustered_selection(path, device):
     """Clustered selections (all selected blocks contiguous inside one 256-block
     route chunk, a different chunk per kv head) are split over the finalize's items
     by count like spread ones: parity with the oracle for clustered, spread and
     single-block masks over three route chunks."""
     c = ("cluster", 41, 4, 4, 128, 64, 40000, 3, "bf16", False, "f32", False)
     name, seed, hkv, g, d, b, p, s, *_ = c
-    announce("fixed-mask clustered selections")
+    announce(f"fixed-mask clustered selections ({path})")
     host, dev = _make(c, device)
     prefix = cb._build_prompt_blocks(dev["k"], dev["v"], b)
     pre = _prefix_np(prefix)

@@ -1262,6 +1262,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD], xbuf[NBUF][2];
     Sub ring[NBUF];
     if (n_sub == 0) return;
+    if constexpr (SRC == kSrcCondFused)  // a wave with no subtile of the item's list
+      if (wave >= n_sub) return;
     ring[0] = seek(wave);
     issue(ring[0], kbuf[0], vbuf[0], xbuf[0]);
     // the loads stay in ring order and ahead of the work on older subtiles (no
@@ -1329,6 +1331,10 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     float m_run = kNegInf, l_run = 0.f;
 
     auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
+      // (the one-launch condition call streams a few subtiles per item: past its list
+      // a wave issues nothing rather than the placeholder loads)
+      if constexpr (SRC == kSrcCondFused)
+        if (sb.k >= n_sub) return;
       const char* kp;
       const char* vp;
       int64_t kts, vts;
@@ -1504,6 +1510,10 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       for (int e = 0; e < DPL; ++e) acc[g][e] = 0.f;
 
     auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
+      // (the one-launch condition call streams a few subtiles per item: past its list
+      // a wave issues nothing rather than the placeholder loads)
+      if constexpr (SRC == kSrcCondFused)
+        if (sb.k >= n_sub) return;
       const char* kp;
       const char* vp;
       int64_t kts, vts;

@@ -84,6 +84,10 @@ def parse():
     ap.add_argument("--kv-layout", default="paired", choices=["split", "paired", "head_paired"],
                     help="K/V pool layout: K and V of a (page, kv head) adjacent in one buffer (paired: "
                          "one 8 KiB run per bf16 page and head), or separate K and V pools (split)")
+    ap.add_argument("--fp8-scales", default="sequence", choices=["page", "sequence"],
+                    help="fp8 pools: the finalize reads the per-page scales ([n_pages, Hkv], two lines per "
+                         "page) or the same scales gathered per sequence (ia.sequence_scales: one line per "
+                         "128-token block); the outputs are the same bits")
     ap.add_argument("--extra", default="c5,c3,c2,cond32k,cond64k,cond128k",
                     help="other BASELINE configs timed in the same run and reported under 'extra' "
                          "(comma list; empty for none)")
@@ -120,10 +124,12 @@ def c3_lengths():
     return [int(x) for x in rng.integers(8192, 65537, size=16)]
 
 
-def make_layer(w, dev, gen, lens, table, n_pages, kv_layout="split"):
+def make_layer(w, dev, gen, lens, table, n_pages, kv_layout="split", fp8_scales="sequence"):
     """One layer's pool, query and summaries.  kv_layout "split": separate K and V
     pools [n_pages, Hkv, page, D]; "paired": one buffer [n_pages, Hkv, 2, page, D]
-    whose K and V of a (page, kv head) are adjacent (pool_k / pool_v are its views)."""
+    whose K and V of a (page, kv head) are adjacent (pool_k / pool_v are its views).
+    fp8 pools carry their per-page scales, and with fp8_scales "sequence" also the
+    per-sequence gather of them that the finalize reads."""
     hkv, page, d = w["hkv"], w["page"], w["d"]
     shape = (n_pages, hkv, page, d)
 
@@ -145,7 +151,7 @@ def make_layer(w, dev, gen, lens, table, n_pages, kv_layout="split"):
         pool_k.copy_((pk.float() / ks[:, :, None, None]).to(torch.float8_e4m3fn))
         pool_v.copy_((pv.float() / vs[:, :, None, None]).to(torch.float8_e4m3fn))
         del pk, pv
-        scales = (ks, vs)
+        scales = (ks, vs, ia.sequence_scales((ks, vs), table)) if fp8_scales == "sequence" else (ks, vs)
     else:
         pool_k, pool_v = pool_pair(torch.bfloat16)
         pool_k.copy_(torch.randn(shape, device=dev, dtype=torch.bfloat16, generator=gen))
@@ -273,7 +279,7 @@ def cpu_baseline(w, L0, table, lens, k_cap, gpu_out, runs=5):
     cpu = torch.device("cpu")
     pk = L0["pool_k"].to(cpu)
     pv = L0["pool_v"].to(cpu)
-    scales = None if L0["scales"] is None else tuple(x.to(cpu) for x in L0["scales"])
+    scales = None if L0["scales"] is None else tuple(x.to(cpu) for x in L0["scales"][:2])
     kb = L0["k_bar"].to(cpu)
     q = L0["q"].to(cpu)
     tab = table.to(cpu)
@@ -333,7 +339,8 @@ def run_topk(name, args, dev, with_dense, with_cpu):
         k_cap = max(ks) + w["ff"] + w["fl"]
     t_setup = time.perf_counter()
     n_layers = rotation_layers(args, topk_bytes_estimate(w, lens))
-    layers = [make_layer(w, dev, gen, lens, table, n_pages, args.kv_layout) for _ in range(n_layers)]
+    layers = [make_layer(w, dev, gen, lens, table, n_pages, args.kv_layout, args.fp8_scales)
+              for _ in range(n_layers)]
     torch.cuda.synchronize()
     print(f"[bench] workload={name} layers={n_layers} setup {time.perf_counter() - t_setup:.1f}s",
           file=sys.stderr, flush=True)

@@ -62,7 +62,16 @@ enum {
  * [Hkv, nb, B, D] (CBT/core.py:383-408) with page_size = B.  Page ids outside
  * [0, n_pages) are skipped (they contribute nothing) instead of being read.
  * For IA_FP8_E4M3, k_scale/v_scale hold one float per (page, kv head) at
- * scale[p * scale_page_stride + h].
+ * scale[p * scale_page_stride + h].  Optionally (fp8 only, else NULL) seq_scale
+ * holds the same two scales gathered per sequence: the (k, v) pair of logical page
+ * lp of batch entry b, kv head h at
+ *   seq_scale[b * seq_scale_b_stride + h * seq_scale_h_stride + 2 * lp + {0, 1}]
+ * for every lp < bt_cols (identity table: lp < n_pages), equal to
+ * (k_scale, v_scale)[block_table[b, lp], h] wherever that page id is valid.  The
+ * pairs of a block's consecutive pages then share a cache line, so the finalize
+ * reads one line per selected block instead of two per page; the per-page arrays
+ * are still required (the summary kernels read them).  The pointer and both strides
+ * must be even (8-byte pairs).
  */
 typedef struct ia_paged_kv {
   const void* k;
@@ -78,6 +87,8 @@ typedef struct ia_paged_kv {
   const float* k_scale;
   const float* v_scale;
   int64_t scale_page_stride;
+  const float* seq_scale; /* optional, fp8: per-sequence (k, v) scale pairs (see above) */
+  int64_t seq_scale_b_stride, seq_scale_h_stride;
 } ia_paged_kv;
 
 /* Query / output geometry: q[b, row, :] at q + b * q_batch_stride + row * q_row_stride,

@@ -11,6 +11,7 @@ from .ops import (  # noqa: F401
     paged_decode,
     paged_kv,
     select_blocks_topk,
+    sequence_scales,
     set_wait_limit,
     sparse_paged_decode,
     sparse_topk_decode,

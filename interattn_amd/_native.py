@@ -55,6 +55,9 @@ class PagedKV(ctypes.Structure):
         ("k_scale", ctypes.c_void_p),
         ("v_scale", ctypes.c_void_p),
         ("scale_page_stride", ctypes.c_int64),
+        ("seq_scale", ctypes.c_void_p),
+        ("seq_scale_b_stride", ctypes.c_int64),
+        ("seq_scale_h_stride", ctypes.c_int64),
     ]
 
 

@@ -51,6 +51,13 @@ int check_kv(const ia_paged_kv* kv, int d) {
     return fail(IA_ERR_INVALID, "kv base pointers must be 16-byte aligned");
   if (kv->dtype == IA_FP8_E4M3 && (!kv->k_scale || !kv->v_scale))
     return fail(IA_ERR_INVALID, "fp8 kv needs k_scale and v_scale");
+  if (kv->seq_scale) {
+    if (kv->dtype != IA_FP8_E4M3) return fail(IA_ERR_INVALID, "seq_scale is for fp8 kv only");
+    if (kv->seq_scale_b_stride < 0 || kv->seq_scale_h_stride < 0 ||
+        (reinterpret_cast<uintptr_t>(kv->seq_scale) | (uintptr_t)kv->seq_scale_b_stride |
+         (uintptr_t)kv->seq_scale_h_stride) % 2 != 0)
+      return fail(IA_ERR_INVALID, "seq_scale pairs must be 8-byte aligned with non-negative even strides");
+  }
   if (kv->block_table && (kv->bt_stride <= 0 || kv->bt_cols < 0 || kv->bt_cols > kv->bt_stride))
     return fail(IA_ERR_INVALID, "block table needs 0 <= bt_cols <= bt_stride and bt_stride > 0");
   if (kv->n_pages < 0) return fail(IA_ERR_INVALID, "n_pages must be >= 0");

@@ -715,6 +715,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ int unit_hi[kMaxUnitsPerItem];
   __shared__ int sub_pg[kMaxSubsPerItem];    // page id of each valid subtile (kSfxPage: suffix)
   __shared__ int sub_info[kMaxSubsPerItem];  // first row in the page (or suffix token) << 5 | valid rows
+  __shared__ int sub_sc[kFp8 ? kMaxSubsPerItem : 1];  // fp8 with sequence scales: 2 x logical page
   __shared__ int wcnt_p[kFinWaves];
   __shared__ int wprog[kFinWaves];  // subtiles consumed per wave
   __shared__ int rc_prefix[SRC == kSrcLists ? kMaxRouteChunks + 1 : 1];
@@ -1086,6 +1087,10 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   const ia_paged_kv& kv = p.kv;
   const int page_size = kv.page_size;
   const int32_t* bt_row = kv.block_table ? kv.block_table + (int64_t)b * kv.bt_stride : nullptr;
+  // fp8 scales gathered per sequence: the (k, v) pairs of this row's logical pages
+  const float* seq_sc =
+      (kFp8 && kv.seq_scale) ? kv.seq_scale + (int64_t)b * kv.seq_scale_b_stride + (int64_t)h * kv.seq_scale_h_stride
+                             : nullptr;
 
   // ---- prologue: token ranges of this item's units (the fused source computes them
   // from its LDS selection where they are used), then one page id per subtile
@@ -1154,7 +1159,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   const int raw0 = u_begin * nsub_u;
   for (int t0 = 0; t0 < nu * nsub_u; t0 += kFinThreads) {
     const int t = t0 + threadIdx.x;
-    int pg = kNoPage, info = 0;
+    int pg = kNoPage, info = 0, sc = 0;
     if (t < nu * nsub_u && raw0 + t >= slot_lo && raw0 + t < slot_hi) {
       const int u = t / nsub_u;
       int lo, hi_raw;
@@ -1181,6 +1186,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
           }
           if (pg < 0 || (int64_t)pg >= kv.n_pages) pg = kNoPage;
           info = ((tok - lp * page_size) << 5) | nv;
+          sc = 2 * lp;
         }
       }
     }
@@ -1194,6 +1200,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
       sub_pg[k] = pg;
       sub_info[k] = info;
+      if constexpr (kFp8) sub_sc[k] = sc;
     }
 #pragma unroll
     for (int w = 0; w < kFinWaves; ++w) n_sub += wcnt_p[w];
@@ -1211,6 +1218,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     int pg;   // page id (kSfxPage: suffix)
     int row;  // first row within the page (suffix: first suffix token)
     int nv;   // valid rows, 1..16
+    int sc;   // fp8: 2 x logical page (the pair's offset in the sequence scales)
   };
   // (wave-uniform: kept in scalar registers).  Past the list the iterator names row 0
   // of subtile 0 with no valid rows: the ring's loads stay unconditional (the same
@@ -1220,7 +1228,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     const int kc = k < n_sub ? k : 0;
     const int info = __builtin_amdgcn_readfirstlane(sub_info[kc]);
     const int pg = __builtin_amdgcn_readfirstlane(sub_pg[kc]);
-    return k < n_sub ? Sub{k, pg, info >> 5, info & 31} : Sub{n_sub, pg, info >> 5, 0};
+    const int sc = kFp8 ? __builtin_amdgcn_readfirstlane(sub_sc[kc]) : 0;
+    return k < n_sub ? Sub{k, pg, info >> 5, info & 31, sc} : Sub{n_sub, pg, info >> 5, 0, sc};
   };
   auto next = [&](const Sub& c) -> Sub { return seek(c.k + kFinWaves); };
 
@@ -1242,13 +1251,17 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   };
 
   // fp8 pages: the (K, V) scales of the subtile's page, loaded unconditionally (the
-  // suffix source, which has none, reads a word of its own row; consume uses 1)
+  // suffix source, which has none, reads a word of its own row; consume uses 1).
+  // With sequence scales both words come from the row's pair for the logical page
+  // (a block's pages share one line); else from the per-page arrays (two lines).
   auto page_scales = [&](const Sub& sb, const char* kp, u32 (&xb)[2]) {
     if constexpr (kFp8) {
       const bool paged = sb.pg >= 0;
       const int64_t at = (int64_t)sb.pg * kv.scale_page_stride + h;
-      xb[0] = *(paged ? reinterpret_cast<const u32*>(kv.k_scale + at) : reinterpret_cast<const u32*>(kp));
-      xb[1] = *(paged ? reinterpret_cast<const u32*>(kv.v_scale + at) : reinterpret_cast<const u32*>(kp));
+      const float* ks = seq_sc ? seq_sc + sb.sc : kv.k_scale + at;
+      const float* vs = seq_sc ? seq_sc + sb.sc + 1 : kv.v_scale + at;
+      xb[0] = *(paged ? reinterpret_cast<const u32*>(ks) : reinterpret_cast<const u32*>(kp));
+      xb[1] = *(paged ? reinterpret_cast<const u32*>(vs) : reinterpret_cast<const u32*>(kp));
     }
   };
 

@@ -103,7 +103,10 @@ def paged_kv(pool_k, pool_v, block_table=None, scales=None):
     if code == N.IA_FP8_E4M3:
         if scales is None:
             raise ValueError("fp8 pools need scales=(k_scale, v_scale), each [n_pages, Hkv] float32")
-        ks, vs = scales
+        if len(scales) not in (2, 3):
+            raise ValueError("scales must be (k_scale, v_scale) or (k_scale, v_scale, sequence_scales)")
+        ks, vs = scales[0], scales[1]
+        seq = scales[2] if len(scales) == 3 else None
         for s_ in (ks, vs):
             _require_cuda(s_)
             if s_.dtype != torch.float32 or tuple(s_.shape) != (n_pages, hkv) or s_.stride(1) != 1:
@@ -114,7 +117,39 @@ def paged_kv(pool_k, pool_v, block_table=None, scales=None):
         kv.v_scale = vs.data_ptr()
         kv.scale_page_stride = int(ks.stride(0))
         keep += [ks, vs]
+        if seq is not None:
+            _require_cuda(seq)
+            cols = int(block_table.shape[1]) if block_table is not None else int(n_pages)
+            if (seq.dtype != torch.float32 or seq.dim() != 4 or seq.shape[1] != hkv or seq.shape[2] < cols
+                    or seq.shape[3] != 2 or seq.stride(3) != 1 or seq.stride(2) != 2):
+                raise ValueError("sequence_scales must be float32 [batch, Hkv, >= max_pages, 2] with contiguous "
+                                 "(k, v) pairs (see sequence_scales())")
+            if seq.stride(0) % 2 or seq.stride(1) % 2 or seq.data_ptr() % 8:
+                raise ValueError("sequence_scales pairs must be 8-byte aligned")
+            kv.seq_scale = seq.data_ptr()
+            kv.seq_scale_b_stride = int(seq.stride(0))
+            kv.seq_scale_h_stride = int(seq.stride(1))
+            keep.append(seq)
+    elif scales is not None and len(scales) == 3:
+        raise ValueError("sequence_scales are for fp8 pools only")
     return kv, keep
+
+
+def sequence_scales(scales, block_table):
+    """fp8 pools: the per-page scales gathered per sequence, ``[batch, Hkv, max_pages, 2]``
+    float32 holding the (k, v) scale pair of each logical page of each sequence, so that a
+    block's consecutive pages share a cache line.  Pass it as the third element of
+    ``scales`` (``scales=(k_scale, v_scale, seq)``) to the decode calls: the outputs are
+    bit-identical, and the finalize reads one scale line per selected block instead of
+    two per page.  Rebuild it whenever the block table or a scale changes (entries past
+    a sequence's valid pages are never read)."""
+    ks, vs = scales[0], scales[1]
+    _check_i32(block_table, "block_table")
+    if block_table.dim() != 2:
+        raise ValueError("block_table must be [batch, max_pages]")
+    pages = block_table.long().clamp(0, max(int(ks.shape[0]) - 1, 0))
+    pair = torch.stack((ks[pages], vs[pages]), dim=-1)  # [batch, max_pages, Hkv, 2]
+    return pair.permute(0, 2, 1, 3).contiguous()
 
 
 def _decode_shape(q, hkv):

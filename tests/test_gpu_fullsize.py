@@ -158,8 +158,11 @@ def test_c5_fullsize_fp8(c4, device):
     # the fused fp8 layer call selects from the same k_bar: same blocks, same output
     fused = ia.sparse_topk_decode(p["q"], k8, v8, p["table"], p["seq"], p["k_bar"], 64, block_size=128,
                                   scales=(ks, vs), workspace={})
+    # and with the scales gathered per sequence (the bench's C5 form): the same bits
+    fused3 = ia.sparse_topk_decode(p["q"], k8, v8, p["table"], p["seq"], p["k_bar"], 64, block_size=128,
+                                   scales=(ks, vs, ia.sequence_scales((ks, vs), p["table"])), workspace={})
     torch.cuda.synchronize()
-    assert torch.equal(fused, got)
+    assert torch.equal(fused, got) and torch.equal(fused3, got)
     err = (got.float() - ref.float()).abs().max().item()
     assert err <= 6e-2, err
     g = HQ // HKV

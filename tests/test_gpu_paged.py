@@ -187,6 +187,14 @@ def test_fp8_paths_match_oracle(c, device):
                                  idx, n_sel, block_size=block, scales=dev["scales"])
     dense = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
                             max_seq_len=max(lens), scales=dev["scales"])
+    # the same scales gathered per sequence (one line per block): the same bits
+    s3 = (*dev["scales"], ia.sequence_scales(dev["scales"], dev["block_table"]))
+    out3 = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                  idx, n_sel, block_size=block, scales=s3)
+    dense3 = ia.paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                             max_seq_len=max(lens), scales=s3)
+    torch.cuda.synchronize()
+    assert torch.equal(out3, out) and torch.equal(dense3, dense)
     # the bf16 reference: same inputs before quantisation
     case_bf = _build(c)
     dev_bf = to_dev(case_bf, device, torch.bfloat16)
@@ -368,6 +376,12 @@ def test_fused_topk_decode_equals_two_step(c, fp8, device):
             n = int(n_sel[i, h])
             assert torch.equal(idx2[i, h, :n], idx[i, h, :n]), (i, h)
     assert torch.equal(out, ref)
+    if fp8:  # the scales gathered per sequence: the same bits
+        s3 = (*dev["scales"], ia.sequence_scales(dev["scales"], dev["block_table"]))
+        out3 = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                     summ["k_bar"], k, scales=s3, workspace={}, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(out3, ref)
 
 
 def test_fused_topk_decode_k_per_seq_and_fallback(device):

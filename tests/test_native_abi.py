@@ -32,8 +32,8 @@ def test_library_exports_every_header_symbol():
 
 
 def test_struct_layouts_match_the_header():
-    # ia_paged_kv: 2 pointers, 2 int32, 7 int64, pointer, 2 int64, 2 pointers, int64
-    assert ctypes.sizeof(N.PagedKV) == 8 * 2 + 4 * 2 + 8 * 7 + 8 + 8 * 2 + 8 * 2 + 8
+    # ia_paged_kv: 2 pointers, 2 int32, 7 int64, pointer, 2 int64, 2 pointers, int64, pointer, 2 int64
+    assert ctypes.sizeof(N.PagedKV) == 8 * 2 + 4 * 2 + 8 * 7 + 8 + 8 * 2 + 8 * 2 + 8 + 8 + 8 * 2
     assert ctypes.sizeof(N.DecodeShape) == 4 * 4 + 8 * 2 + 8
     # ia_block_summaries: 4 pointers, 3 int32 (+pad), 3 pointers, 2 int32
     assert ctypes.sizeof(N.BlockSummaries) == 8 * 4 + 4 * 4 + 8 * 3 + 4 * 2
@@ -122,3 +122,41 @@ def test_noalloc_rejects_calls_beyond_its_scratch_before_launching():
                                                N.IA_BF16, None, None, None)
         assert rc == N.IA_ERR_WORKSPACE, (what, lib.ia_last_error())
         assert "scratch" in lib.ia_last_error().decode(), what
+
+
+def test_sequence_scales_are_checked_before_launching():
+    # per-sequence scale pairs on a bf16 pool, and odd (unaligned) pair strides on an
+    # fp8 pool: both rejected by the argument checks
+    lib = N.lib()
+    sh = N.DecodeShape(batch=1, n_q_heads=32, n_kv_heads=8, head_dim=128, q_batch_stride=32 * 128, q_row_stride=128,
+                       q_dtype=N.IA_BF16)
+    kv = N.PagedKV(k=256, v=256, dtype=N.IA_BF16, page_size=16, n_pages=4, k_page_stride=8 * 16 * 128,
+                   k_head_stride=16 * 128, k_token_stride=128, v_page_stride=8 * 16 * 128, v_head_stride=16 * 128,
+                   v_token_stride=128, seq_scale=256, seq_scale_b_stride=64, seq_scale_h_stride=8)
+    rc = lib.ia_paged_decode(sh, 256, kv, 256, 64, 0.1, 256, N.IA_BF16, 256, 1 << 20, None)
+    assert rc == N.IA_ERR_INVALID and b"seq_scale" in lib.ia_last_error()
+    kv.dtype = N.IA_FP8_E4M3
+    kv.k_scale = kv.v_scale = 256
+    kv.scale_page_stride = 8
+    kv.seq_scale_h_stride = 3
+    rc = lib.ia_paged_decode(sh, 256, kv, 256, 64, 0.1, 256, N.IA_BF16, 256, 1 << 20, None)
+    assert rc == N.IA_ERR_INVALID and b"seq_scale" in lib.ia_last_error()
+
+
+def test_sequence_scales_gather_the_page_scales():
+    import torch
+
+    import interattn_amd as ia
+
+    g = torch.Generator().manual_seed(3)
+    ks, vs = torch.rand(10, 4, generator=g), torch.rand(10, 4, generator=g)
+    table = torch.tensor([[3, 7, 1, -1], [0, 9, 2, 5]], dtype=torch.int32)
+    seq = ia.sequence_scales((ks, vs), table)
+    assert seq.shape == (2, 4, 4, 2) and seq.is_contiguous()
+    for b in range(2):
+        for lp in range(4):
+            pg = int(table[b, lp])
+            if pg < 0:
+                continue  # never read: the finalize skips invalid pages
+            for h in range(4):
+                assert float(seq[b, h, lp, 0]) == float(ks[pg, h]) and float(seq[b, h, lp, 1]) == float(vs[pg, h])

@@ -448,15 +448,30 @@ IA_API int ia_sparse_topk_decode_noalloc(const ia_decode_shape* shape, const voi
                                          int32_t* n_sel, void* stream);
 
 /*
- * Bound of every wait of one workgroup on another inside ia_sparse_topk_decode, in
- * ticks of the GPU's 100 MHz constant clock (default 2,000,000 = 20 ms; a negative
- * value restores it).  Returns the previous bound.  Applies to calls issued after
- * it on any thread.  A bound of 0 makes every waiting item compute the missing
- * block scores itself (the tests use it to exercise that path).  The merging item's
- * reads of partials whose items have finished wait at least 20 ms for their stores
+ * Bound of every wait of one workgroup on another inside the one-launch calls
+ * (ia_sparse_topk_decode and its no-alloc form, ia_condition_decode_fused,
+ * ia_fixed_mask_decode_fused), in ticks of the GPU's 100 MHz constant clock
+ * (default 20,000 = 200 us, ~15x the longest prologue; a negative value restores
+ * it).  Returns the previous bound.  Applies to calls issued after it on any
+ * thread.  A wait that reaches the bound makes the waiting item compute the missing
+ * block scores or statistics itself: the same results, later (a bound of 0 makes
+ * every such item do so; the tests use it to exercise that path).  So when the
+ * launch's workgroups are not all resident together (other work sharing the GPU),
+ * a call costs at most about this bound more.  The merging item's reads of partials
+ * whose items have finished (their stores already issued) wait at least 20 ms
  * whatever this bound.  No reference counterpart.
  */
 IA_API int64_t ia_set_wait_limit(int64_t ticks);
+
+/*
+ * Diagnostic: the number of waits of the one-launch calls that reached their bound
+ * on the current device since the process started or the last reset (reset != 0
+ * zeroes the count after reading it).  Each was a hand-off computed by the waiting
+ * item itself (same results), or a merge read that still missed after 20 ms (the
+ * row's output is then NaN).  Reads device memory synchronously: not for a hot loop
+ * or graph capture.  No reference counterpart.
+ */
+IA_API int64_t ia_wait_fallbacks(int32_t reset);
 
 /* Most split-K items per (b, h) the two decode entry points use for the given
  * workload (the stride of the partials); size the decode workspace with it.

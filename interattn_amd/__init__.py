@@ -16,6 +16,7 @@ from .ops import (  # noqa: F401
     sparse_paged_decode,
     sparse_topk_decode,
     update_block_summaries,
+    wait_fallbacks,
     workspace_tensor,
 )
 

@@ -151,6 +151,7 @@ SIGNATURES = {
          _P, _I32, _I32, _I32, _I32, _F, _P, _I32, _P, _P, _P],
     ),
     "ia_set_wait_limit": (_I64, [_I64]),
+    "ia_wait_fallbacks": (_I64, [_I32]),
     "ia_select_topk_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "ia_select_topk": (
         ctypes.c_int,

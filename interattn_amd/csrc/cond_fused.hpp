@@ -271,6 +271,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     if (miss) L.missing = 1u;
     __syncthreads();
     if (L.missing) {  // a partner's partial missed the bound: every other range here
+      if (t == 0) note_wait_fallback();
       for (int i = 0; i < n_it; ++i) {
         if (i == item) continue;
         const int ilo = cond_range_lo(i, nb, n_it), ihi = cond_range_lo(i + 1, nb, n_it);

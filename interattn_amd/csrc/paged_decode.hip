@@ -8,7 +8,10 @@
 namespace ia {
 
 namespace {
-constexpr int64_t kDefaultWaitTicks = 2000000;  // 20 ms of the 100 MHz clock
+// 200 us of the 100 MHz clock: a partner workgroup that runs alongside publishes within
+// ~15 us of the launch; one that is not resident (the GPU shared with other work) costs
+// the waiting item this bound and then its own computation of the missing data
+constexpr int64_t kDefaultWaitTicks = 20000;
 std::atomic<int64_t> g_wait_ticks{kDefaultWaitTicks};
 }  // namespace
 
@@ -330,6 +333,11 @@ int ia_sparse_topk_decode(const ia_decode_shape* shape, const void* q, const ia_
 }
 
 int64_t ia_set_wait_limit(int64_t ticks) { return ia::set_wait_limit_ticks(ticks); }
+
+int64_t ia_wait_fallbacks(int32_t reset) {
+  const bool r = reset != 0;
+  return (int64_t)(ia::wait_fallbacks_bf16(r) + ia::wait_fallbacks_f32(r) + ia::wait_fallbacks_fp8(r));
+}
 
 size_t ia_paged_decode_workspace_size(int32_t batch, int32_t n_kv_heads, int32_t group, int32_t head_dim,
                                       int32_t max_items) {

@@ -41,4 +41,6 @@ int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipSt
   return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination");
 }
 
+uint64_t wait_fallbacks_bf16(bool reset) { return tu_wait_fallbacks(reset); }
+
 }  // namespace ia

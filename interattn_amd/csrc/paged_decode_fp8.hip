@@ -34,4 +34,6 @@ int dispatch_fp8(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStr
   return fail(IA_ERR_UNSUPPORTED, "head_dim / group combination");
 }
 
+uint64_t wait_fallbacks_fp8(bool reset) { return tu_wait_fallbacks(reset); }
+
 }  // namespace ia

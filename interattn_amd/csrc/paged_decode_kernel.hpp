@@ -49,6 +49,28 @@
 
 namespace ia {
 
+// Waits of one workgroup on another that reached their bound: the waiting workgroup
+// then computed the missing data itself (score and statistics hand-offs: same
+// results, later) or, for a merge read of a finished item's partial, wrote NaN.
+// One counter per device in each translation unit that instantiates the kernels
+// (device variables are not shared between translation units), summed by
+// ia_wait_fallbacks.  A vector atomic, taken only on that rare path.
+static __device__ u32 g_wait_fallbacks[1];
+__device__ __forceinline__ void note_wait_fallback() {
+  __hip_atomic_fetch_add(g_wait_fallbacks, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Host: this translation unit's counter on the current device (a synchronous read;
+// reset to zero when `reset`).
+static inline uint64_t tu_wait_fallbacks(bool reset) {
+  u32 v = 0u;
+  if (hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_wait_fallbacks), sizeof(v), 0, hipMemcpyDeviceToHost) != hipSuccess) return 0;
+  if (reset) {
+    const u32 zero = 0u;
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(g_wait_fallbacks), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+  }
+  return v;
+}
+
 // kRing: register buffers in the load pipeline (subtiles in flight = kRing - 1),
 // sized so a wave stays within 256 registers (two waves per SIMD).
 struct KvBf16 {
@@ -650,7 +672,9 @@ __device__ __forceinline__ void fused_merge_tagged(const DecodeParams& p, int b,
       __builtin_amdgcn_s_sleep(1);
       v = ld_agent_u64(ptr);
     }
-    return (u32)(v >> 32) == tag ? __uint_as_float((u32)v) : __builtin_nanf("");
+    if ((u32)(v >> 32) == tag) return __uint_as_float((u32)v);
+    note_wait_fallback();
+    return __builtin_nanf("");
   };
   // (m, l) of every slot, staged in LDS
   if (threadIdx.x < kMergeGroup * G * 2) {
@@ -989,6 +1013,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
         __syncthreads();
         staged = merge_todo[0] == 0u;
         if (!staged) {  // an entry missed the bound: the other items' blocks here
+          if (threadIdx.x == 0) note_wait_fallback();
           score_range(0, own_lo);
           score_range(own_hi, nbs);
         }
@@ -2135,6 +2160,10 @@ int64_t set_wait_limit_ticks(int64_t ticks);
 int dispatch_bf16(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
 int dispatch_f32(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
 int dispatch_fp8(const DecodeParams& p, int d, int g, int src, dim3 grid, hipStream_t st, int* resident);
+// Their translation units' wait-fallback counters (tu_wait_fallbacks).
+uint64_t wait_fallbacks_bf16(bool reset);
+uint64_t wait_fallbacks_f32(bool reset);
+uint64_t wait_fallbacks_fp8(bool reset);
 
 }  // namespace ia
 

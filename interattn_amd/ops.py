@@ -295,9 +295,20 @@ def _block_keys(k_bar, score):
 
 
 def set_wait_limit(ticks):
-    """Bound (100 MHz clock ticks) of every wait between the workgroups of a fused
-    top-k call; a negative value restores the default.  Returns the previous bound."""
+    """Bound (100 MHz clock ticks) of every wait between the workgroups of a one-launch
+    call (default 20,000 = 200 us); a negative value restores the default.  A wait that
+    reaches it makes the waiting workgroup compute the missing data itself (same
+    results).  Returns the previous bound."""
     return int(N.lib().ia_set_wait_limit(int(ticks)))
+
+
+def wait_fallbacks(reset=False):
+    """Diagnostic: waits of the one-launch calls on the current device that reached their
+    bound since the process started or the last ``reset`` (each one's workgroup computed
+    the missing scores or statistics itself).  Nonzero in normal operation means the
+    launches' workgroups were not all resident together (other work on the GPU).  Reads
+    device memory synchronously."""
+    return int(N.lib().ia_wait_fallbacks(1 if reset else 0))
 
 def select_blocks_topk(q, k_bar, seq_lens, k, *, block_size, forced_first=0, forced_last=0,
                        forced_in_k=False, k_cap=None, k_per_seq=None, return_scores=False, score="mean",

@@ -75,6 +75,8 @@ def test_one_launch_handoff_fallback_is_exact(name, device, one_launch):
     sfx_len = torch.full((1,), s, device=device, dtype=torch.int32)
     lib = N.lib()
     res = []
+    lib.ia_wait_fallbacks(1)
+    counts = []
     for limit in (-1, 0):  # default bound, then 0: every item computes every partial itself
         prev = lib.ia_set_wait_limit(limit)
         try:
@@ -86,9 +88,13 @@ def test_one_launch_handoff_fallback_is_exact(name, device, one_launch):
             torch.cuda.synchronize()
         finally:
             lib.ia_set_wait_limit(prev)
+        counts.append(lib.ia_wait_fallbacks(1))
         res.append((out.clone(), ws["selected_rows"].clone()))
     assert torch.equal(res[0][1], res[1][1]), "selection depends on the hand-off"
     assert torch.equal(res[0][0], res[1][0]), "output depends on the hand-off"
+    # the diagnostic: no fallback at the default bound with every workgroup resident
+    print(f"[{name}] wait fallbacks: default bound {counts[0]}, bound 0 {counts[1]}", flush=True)
+    assert counts[0] == 0
 
 
 def test_one_launch_workspace_across_lengths_and_graph_replays(device, one_launch):

@@ -531,17 +531,24 @@ def test_fused_handoff_fallback_is_exact(name, device):
         refs.append(ia.sparse_paged_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
                                            idx, n_sel, block_size=block).clone())
     ws = {}
+    ia.wait_fallbacks(reset=True)
     previous = ia.set_wait_limit(0)
     try:
         got0 = [ia.sparse_topk_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
                                       summ["k_bar"], k, workspace=ws, **kw).clone() for q in qs]
     finally:
         ia.set_wait_limit(previous)
+    torch.cuda.synchronize()
+    n0 = ia.wait_fallbacks(reset=True)
     got = [ia.sparse_topk_decode(q, dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
                                  summ["k_bar"], k, workspace=ws, **kw).clone() for q in qs]
     torch.cuda.synchronize()
     for r, a, b_ in zip(refs, got0, got):
         assert torch.equal(a, r) and torch.equal(b_, r)
+    # the diagnostic counts the bound-0 run's fallbacks (none when every row scores
+    # itself), and none at the default bound with every workgroup resident
+    print(f"[{name}] wait fallbacks at bound 0: {n0}", flush=True)
+    assert n0 >= 0 and ia.wait_fallbacks() == 0
 
 
 @pytest.mark.parametrize("rows", [(4, 32, 8), (7, 16, 4)], ids=["32rows", "28rows"])

@@ -22,6 +22,8 @@ build runs on one GPU.
 """
 
 import argparse
+import glob
+import hashlib
 import json
 import math
 import os
@@ -477,27 +479,53 @@ def run_topk(name, args, dev, with_dense, with_cpu):
                 cpu=cpu)
 
 
+def kernel_sources_sha16():
+    """Hash of the kernel sources (csrc/*.hip, csrc/*.hpp, include/*.h): the profiles
+    record it, so a profile taken on other kernels is recognised as stale."""
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(ROOT, "interattn_amd", "csrc", "*.hip")) +
+                   glob.glob(os.path.join(ROOT, "interattn_amd", "csrc", "*.hpp")) +
+                   glob.glob(os.path.join(ROOT, "include", "*.h")))
+    for f in files:
+        h.update(os.path.relpath(f, ROOT).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def profile_record(name):
+    """profiles/hbm_traffic.json's record of a workload, or None when there is none or
+    it was taken on other kernel sources (then its figures are not reported)."""
+    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(tpath):
+        return None
+    rec = json.load(open(tpath)).get(name)
+    if not rec or rec.get("sources_sha16") != kernel_sources_sha16():
+        return None
+    return rec
+
+
 def traffic_of(name):
     """HBM bytes per layer call measured by rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (copy-calibrated), from profiles/hbm_traffic.json."""
-    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    if os.path.exists(tpath):
-        rec = json.load(open(tpath)).get(name)
-        if rec:
-            return int(round(rec["hbm_read_bytes"] + rec["hbm_write_bytes"])), rec["source"]
+    (copy-calibrated), from profiles/hbm_traffic.json when it was taken on these
+    kernel sources."""
+    rec = profile_record(name)
+    if rec:
+        return int(round(rec["hbm_read_bytes"] + rec["hbm_write_bytes"])), rec["source"]
     return None, None
 
 
 def kernel_avg_of(name, total_bytes):
     """The dominant kernel's rocprofv3 trace average (profiles/hbm_traffic.json, taken
-    over the same settled calls) and the roofline fraction it gives on its own."""
-    tpath = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    rec = json.load(open(tpath)).get(name) if os.path.exists(tpath) else None
+    over the same settled calls on these kernel sources) and the roofline fraction it
+    gives on its own; a note instead when the profile is missing or stale."""
+    rec = profile_record(name)
     if not rec or not rec.get("kernel_avg_us"):
-        return {}
+        return {"rocprof_note": "no profile of these kernel sources in profiles/hbm_traffic.json"}
     avg = float(rec["kernel_avg_us"])
     return {"rocprof_kernel_avg_us": avg,
-            "rocprof_kernel_frac": round(total_bytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+            "rocprof_kernel_frac": round(total_bytes / (avg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "rocprof_sources_sha16": rec["sources_sha16"]}
 
 
 def config_of(name, r):

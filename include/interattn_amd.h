@@ -249,7 +249,11 @@ IA_API int ia_paged_decode(const ia_decode_shape* shape, const void* q, const ia
  * [batch, Hkv, nb] and v_norm_all [batch, Hkv] float32, counts [batch, nb]
  * int32 (valid tokens per block; 0 = no block).  block_size = tokens per block.
  * This is the prefix dict of _build_prompt_blocks (CBT/core.py:449-500) with a
- * batch dimension.
+ * batch dimension.  bounds_packed = 1: the bounds are the reference's packed
+ * k_bounds instead (CBT/core.py:490-499, CONDITION_BLOCK_TMA_BOUNDS=1): k_max points
+ * to [batch, Hkv, nb, 2 D] whose element pair (k_max, k_min) of dimension e sits at
+ * [2e, 2e + 1], and k_min is not read (the statistics read each lane's pairs with
+ * the same two 16-byte loads as the separate rows).
  */
 typedef struct ia_block_summaries {
   const void* k_bar;
@@ -262,6 +266,7 @@ typedef struct ia_block_summaries {
   const int32_t* counts;
   int32_t nb;
   int32_t block_size;
+  int32_t bounds_packed; /* 0: k_max and k_min rows; 1: packed k_bounds at k_max */
 } ia_block_summaries;
 
 /*

@@ -87,6 +87,7 @@ class BlockSummaries(ctypes.Structure):
         ("counts", ctypes.c_void_p),
         ("nb", ctypes.c_int32),
         ("block_size", ctypes.c_int32),
+        ("bounds_packed", ctypes.c_int32),
     ]
 
 

@@ -124,8 +124,10 @@ def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=None, mixed=
     """Prompt summaries (CBT/core.py:449-500): the same dict keys, built by the HIP
     summary kernel over the padded block view.  Storage dtypes as
     ``summary_storage_dtypes`` (keywords, else the reference's environment switches);
-    with ``CONDITION_BLOCK_TMA_BOUNDS=1`` the packed ``k_bounds [Hkv, nb, 2D]``
-    (k_max, k_min interleaved) is added as the reference does (CBT/core.py:490-499)."""
+    with ``CONDITION_BLOCK_TMA_BOUNDS=1`` the bounds are stored as the packed
+    ``k_bounds [Hkv, nb, 2D]`` (k_max, k_min interleaved per dimension) and ``k_max`` /
+    ``k_min`` become views of it, as the reference does (CBT/core.py:490-499); the
+    statistics kernels then read the packed rows."""
     _require_cuda(k_all, v_all)
     if block_size <= 0 or block_size % 16:
         raise ValueError("block_size must be a positive multiple of 16")
@@ -175,7 +177,9 @@ def _build_prompt_blocks(k_all, v_all, block_size, *, summary_dtype=None, mixed=
         "_block_size": int(block_size),
     }
     if os.environ.get("CONDITION_BLOCK_TMA_BOUNDS") == "1":
-        res["k_bounds"] = torch.stack((res["k_max"], res["k_min"]), dim=-1).flatten(2).contiguous()
+        bounds = torch.stack((res["k_max"], res["k_min"]), dim=-1).flatten(2).contiguous()
+        pairs = bounds.view(*res["k_max"].shape, 2)
+        res["k_bounds"], res["k_max"], res["k_min"] = bounds, pairs[..., 0], pairs[..., 1]
     return res
 
 
@@ -195,12 +199,22 @@ def _summaries_desc(prefix, n_kv_heads, head_dim):
         keep.append(t)
         return t
 
-    k_bar, k_max, k_min, v_bar = arr("k_bar"), arr("k_max"), arr("k_min"), arr("v_bar")
+    k_bar, v_bar = arr("k_bar"), arr("v_bar")
     nb = int(k_bar.shape[-2])
     if tuple(k_bar.shape) != (n_kv_heads, nb, head_dim):
         raise ValueError(f"k_bar must be [Hkv, nb, D] = {(n_kv_heads, nb, head_dim)}, got {tuple(k_bar.shape)}")
-    if k_max.dtype != k_min.dtype:
-        raise ValueError("k_max and k_min must share a dtype")
+    bounds = prefix.get("k_bounds")
+    if bounds is not None:
+        # the packed bounds (CBT/core.py:490-499): read in place, k_max / k_min are views
+        if tuple(bounds.shape) != (n_kv_heads, nb, 2 * head_dim) or not bounds.is_contiguous():
+            raise ValueError(f"k_bounds must be contiguous [Hkv, nb, 2D] = {(n_kv_heads, nb, 2 * head_dim)}")
+        keep.append(bounds)
+        k_max = k_min = bounds
+        sm.bounds_packed = 1
+    else:
+        k_max, k_min = arr("k_max"), arr("k_min")
+        if k_max.dtype != k_min.dtype:
+            raise ValueError("k_max and k_min must share a dtype")
     counts = prefix.get("_counts_i32")
     if counts is None:
         counts = prefix["block_valid_counts"].to(torch.int32).contiguous()

@@ -123,14 +123,14 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     const int nsteps = (rm + 31) / 32;
     const int cl = t < rm ? p.c_counts[(int64_t)b * nb + rlo + t] : 0;
     for (int s0 = 0; s0 < nsteps; s0 += kSteps) {
-      SumRow<DPL, SBF> kb[kSteps], kx[MASK ? 1 : kSteps], kn[MASK ? 1 : kSteps];
+      SumRow<DPL, SBF> kb[kSteps];
+      BoundRows<DPL, SBF> kx[MASK ? 1 : kSteps];
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {
         const int64_t off = (vrow + rlo + min(32 * (s0 + u) + 4 * wave + r, rm - 1)) * D + c16 * DPL;
         kb[u].load(p.c_kbar, off, kbf);
         if constexpr (!MASK) {
-          kx[u].load(p.c_kmax, off, xbf);
-          kn[u].load(p.c_kmin, off, xbf);
+          kx[u].load(p.c_kmax, p.c_kmin, off, xbf, p.c_bounds_packed);
         }
       }
       if (s0 == 0 && t < kCondItemBlocks) L.lc[t] = cl > 0 ? __logf((float)cl) : kNegInf;
@@ -151,7 +151,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
             kbv[e] = round_if(kb[u].at(e, kbf), p.c_rep_bf16 && !kbf);
             ksum[e] = kdif[e] = 0.f;
           } else {
-            const float hx = kx[u].at(e, xbf), ln = kn[u].at(e, xbf);
+            const float hx = kx[u].mx(e, xbf), ln = kx[u].mn(e, xbf);
             ksum[e] = hx + ln;
             kdif[e] = hx - ln;
             kbv[e] = kb[u].at(e, kbf);

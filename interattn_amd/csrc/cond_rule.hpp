@@ -91,4 +91,27 @@ struct SumRow {
   }
 };
 
+// The elementwise key bounds of one summary row slice (DPL elements at element offset
+// off of a [.., D] row layout): k_max and k_min rows, or the packed k_bounds row of
+// 2 D elements whose pair (k_max, k_min) of dimension e sits at [2e, 2e + 1] (the
+// reference's layout, CBT/core.py:490-499).  Both forms take the same two loads of DPL
+// elements, chosen without a branch (the two rows' slices, or the two halves of the
+// lane's packed slice); mx(e) / mn(e) pick the elements.
+template <int DPL, int BF16 = 0>
+struct BoundRows {
+  SumRow<DPL, BF16> a, b;
+  bool packed;
+  __device__ __forceinline__ void load(const void* kmax, const void* kmin, int64_t off, bool bf16, bool pk) {
+    packed = pk;
+    a.load(kmax, pk ? 2 * off : off, bf16);
+    b.load(pk ? kmax : kmin, pk ? 2 * off + DPL : off, bf16);
+  }
+  __device__ __forceinline__ float mx(int e, bool bf16) const {
+    return packed ? (e < DPL / 2 ? a.at(2 * e, bf16) : b.at(2 * e - DPL, bf16)) : a.at(e, bf16);
+  }
+  __device__ __forceinline__ float mn(int e, bool bf16) const {
+    return packed ? (e < DPL / 2 ? a.at(2 * e + 1, bf16) : b.at(2 * e + 1 - DPL, bf16)) : b.at(e, bf16);
+  }
+};
+
 }  // namespace ia

@@ -45,6 +45,7 @@ struct CondParams {
   const void* k_bar;
   const void* k_max;
   const void* k_min;
+  int32_t bounds_packed;  // k_max is the packed k_bounds (pairs per dimension), k_min unused
   const void* v_bar;
   const float* v_norm_max;  // [batch, Hkv, nb]
   const float* v_norm_all;  // [batch, Hkv]
@@ -101,6 +102,29 @@ struct RawRow {
   __device__ __forceinline__ float operator[](int e) const {
     if constexpr (BF16) return (e & 1) ? bf16_hi(w[e >> 1]) : bf16_lo(w[e >> 1]);
     else return __uint_as_float(w[e]);
+  }
+};
+
+// k_max / k_min of one row slice: the separate rows, or the packed k_bounds row whose
+// pair (k_max, k_min) of dimension e sits at [2e, 2e + 1] (CBT/core.py:490-499).  The
+// same two loads of DPL elements either way, chosen without a branch.
+template <bool BF16, int DPL>
+struct RawBounds {
+  RawRow<BF16, DPL> a, b;
+  bool packed;
+  __device__ __forceinline__ void load(const void* kmax, const void* kmin, int64_t off, bool pk) {
+    packed = pk;
+    a.load(kmax, pk ? 2 * off : off);
+    b.load(pk ? kmax : kmin, pk ? 2 * off + DPL : off);
+  }
+  __device__ __forceinline__ void zero() {
+    a.zero();
+    b.zero();
+    packed = false;
+  }
+  __device__ __forceinline__ float mx(int e) const { return packed ? (e < DPL / 2 ? a[2 * e] : b[2 * e - DPL]) : a[e]; }
+  __device__ __forceinline__ float mn(int e) const {
+    return packed ? (e < DPL / 2 ? a[2 * e + 1] : b[2 * e + 1 - DPL]) : b[e];
   }
 };
 
@@ -192,16 +216,14 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
   const bool inb = j < p.nb;
   const int cnt = inb ? p.counts[(int64_t)b * p.nb + j] : 0;
   RawRow<KBH, DPL> rb;
-  RawRow<BDH, DPL> rh, rl;
+  RawBounds<BDH, DPL> rx;
   if (inb) {
     const int64_t off = (vbase + j) * D + c16 * DPL;
     rb.load(p.k_bar, off);
-    rh.load(p.k_max, off);
-    rl.load(p.k_min, off);
+    rx.load(p.k_max, p.k_min, off, p.bounds_packed);
   } else {
     rb.zero();
-    rh.zero();
-    rl.zero();
+    rx.zero();
   }
   // q rows h*G + g at dims c16*DPL ..: one 16-byte (bf16) or DPL/4 16-byte (f32) loads
   u32 qw[G][DPL];
@@ -226,8 +248,8 @@ __global__ __launch_bounds__(256) void ia_condition_block_selection_stats(CondPa
   float ksum[DPL], kdif[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
-    ksum[e] = rh[e] + rl[e];
-    kdif[e] = rh[e] - rl[e];
+    ksum[e] = rx.mx(e) + rx.mn(e);
+    kdif[e] = rx.mx(e) - rx.mn(e);
   }
   float ps[G], pa[G], pb[G];
 #pragma unroll
@@ -579,7 +601,9 @@ __global__ __launch_bounds__(256) void ia_condition_block_route(CondParams p) {
 
 int check_summaries(const ia_block_summaries* sm, bool need_bounds, bool need_v) {
   if (!sm || !sm->k_bar || !sm->counts) return fail(IA_ERR_INVALID, "summaries need k_bar and counts");
-  if (need_bounds && (!sm->k_max || !sm->k_min)) return fail(IA_ERR_INVALID, "summaries need k_max and k_min");
+  if (sm->bounds_packed != 0 && sm->bounds_packed != 1) return fail(IA_ERR_INVALID, "bounds_packed must be 0 or 1");
+  if (need_bounds && (!sm->k_max || (!sm->bounds_packed && !sm->k_min)))
+    return fail(IA_ERR_INVALID, "summaries need k_max and k_min (or packed bounds at k_max)");
   if (need_v && (!sm->v_bar || !sm->v_norm_max || !sm->v_norm_all))
     return fail(IA_ERR_INVALID, "summaries need v_bar, v_norm_max and v_norm_all");
   const int32_t dts[3] = {sm->k_bar_dtype, sm->bounds_dtype, sm->v_bar_dtype};
@@ -587,7 +611,7 @@ int check_summaries(const ia_block_summaries* sm, bool need_bounds, bool need_v)
     if (dt != IA_F32 && dt != IA_BF16) return fail(IA_ERR_INVALID, "summary dtypes must be IA_F32 or IA_BF16");
   if (sm->nb < 0 || sm->block_size <= 0 || sm->block_size % 16 || sm->block_size > 32768)
     return fail(IA_ERR_INVALID, "nb must be >= 0 and block_size a positive multiple of 16, at most 32768");
-  const void* ptrs[4] = {sm->k_bar, sm->k_max, sm->k_min, sm->v_bar};
+  const void* ptrs[4] = {sm->k_bar, sm->k_max, sm->bounds_packed ? nullptr : sm->k_min, sm->v_bar};
   for (const void* q : ptrs)
     if (reinterpret_cast<uintptr_t>(q) % 16) return fail(IA_ERR_INVALID, "summary arrays must be 16-byte aligned");
   return IA_OK;
@@ -601,7 +625,8 @@ CondParams cond_params(const ia_decode_shape* shape, const void* q, const ia_blo
   p.q_f32 = shape->q_dtype == IA_F32;
   p.k_bar = sm->k_bar;
   p.k_max = sm->k_max;
-  p.k_min = sm->k_min;
+  p.k_min = sm->bounds_packed ? sm->k_max : sm->k_min;
+  p.bounds_packed = sm->bounds_packed;
   p.v_bar = sm->v_bar;
   p.v_norm_max = sm->v_norm_max;
   p.v_norm_all = sm->v_norm_all;
@@ -931,7 +956,8 @@ int run_condition_fused(const uint8_t* mask, const ia_decode_shape* shape, const
   p.wait_ticks = wait_limit_ticks();
   p.c_kbar = sm->k_bar;
   p.c_kmax = sm->k_max;
-  p.c_kmin = sm->k_min;
+  p.c_kmin = sm->bounds_packed ? sm->k_max : sm->k_min;
+  p.c_bounds_packed = sm->bounds_packed;
   p.c_vbar = sm->v_bar;
   p.c_kbar_bf16 = sm->k_bar_dtype == IA_BF16;
   p.c_bounds_bf16 = sm->bounds_dtype == IA_BF16;

@@ -197,6 +197,7 @@ struct DecodeParams {
   const void* c_kmin;
   const void* c_vbar;
   int32_t c_kbar_bf16, c_bounds_bf16, c_vbar_bf16;
+  int32_t c_bounds_packed;  // k_max is the packed k_bounds (pairs per dimension), k_min unused
   const float* c_vnorm_max;
   const float* c_vnorm_all;
   const int32_t* c_counts;

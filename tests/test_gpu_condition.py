@@ -251,6 +251,43 @@ def test_condition_decode_vs_oracle(c, path, device):
         assert {k_: int(v_) for k_, v_ in stats.items()} == ref_stats
 
 
+@pytest.mark.parametrize("name", ["f32_b64_g4", "bf16_mixed_b32_mass", "bf16_c1_like"])
+def test_packed_bounds_equal_separate(name, path, device, monkeypatch):
+    """The reference's packed bounds (CONDITION_BLOCK_TMA_BOUNDS=1: k_bounds [Hkv, nb,
+    2D] with k_max / k_min as views, CBT/core.py:490-499) read in place by the
+    statistics: statistics, selection and output equal the separate rows' bit for bit."""
+    c = next(x for x in CASES if x[0] == name)
+    _, seed, hkv, g, d, b, p, s, dt, mixed, kbd, mass = c
+    announce(f"packed bounds {name} ({path})")
+    host, dev = _make(c, device)
+    kbt = torch.bfloat16 if kbd == "bf16" else torch.float32
+    monkeypatch.delenv("CONDITION_BLOCK_TMA_BOUNDS", raising=False)
+    sep = cb._build_prompt_blocks(dev["k"], dev["v"], b, mixed=mixed, k_bar_dtype=kbt)
+    monkeypatch.setenv("CONDITION_BLOCK_TMA_BOUNDS", "1")
+    packed = cb._build_prompt_blocks(dev["k"], dev["v"], b, mixed=mixed, k_bar_dtype=kbt)
+    monkeypatch.delenv("CONDITION_BLOCK_TMA_BOUNDS")
+    assert "k_bounds" in packed and not packed["k_max"].is_contiguous()
+    assert packed["k_max"].data_ptr() == packed["k_bounds"].data_ptr()
+    assert torch.equal(packed["k_max"], sep["k_max"]) and torch.equal(packed["k_min"], sep["k_min"])
+    pre = _prefix_np(sep)
+    _, mean, _ = _oracle_stats(host["q"][:, :, 0].reshape(-1, d), pre, g, mass)
+    vals = np.unique(mean[mean > 0])
+    eps = float(0.5 * (vals[int(0.85 * len(vals))] + vals[int(0.85 * len(vals)) + 1]))
+    st = [cb._run_condition_block_selection_stats(dev["q"], pf, term1_mass_exp=mass) for pf in (sep, packed)]
+    for a, b_ in zip(st[0][1:5], st[1][1:5]):
+        assert torch.equal(a, b_), "statistics depend on the bounds layout"
+    sfx_len = torch.full((1,), s, device=device, dtype=torch.int32)
+    res = []
+    for pf in (sep, packed):
+        ws = {}
+        out, _ = cb._condition_block_decode_output(
+            q_grouped=dev["q"], prompt_prefix=pf, k_suffix=dev["ks"], v_suffix=dev["vs"], suffix_len_dev=sfx_len,
+            block_size=b, eps=eps, prompt_len=p, attention_dtype=torch.float32, workspace=ws, term1_mass_exp=mass)
+        torch.cuda.synchronize()
+        res.append((out.clone(), ws["selected_rows"].clone()))
+    assert torch.equal(res[0][1], res[1][1]) and torch.equal(res[0][0], res[1][0])
+
+
 def test_condition_suffix_length_on_device(path, device):
     """The suffix length is read on the device: one buffer of capacity 64 serves
     lengths 0, 1 and 40 (the captured decode step advances it in place)."""

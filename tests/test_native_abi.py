@@ -35,8 +35,8 @@ def test_struct_layouts_match_the_header():
     # ia_paged_kv: 2 pointers, 2 int32, 7 int64, pointer, 2 int64, 2 pointers, int64, pointer, 2 int64
     assert ctypes.sizeof(N.PagedKV) == 8 * 2 + 4 * 2 + 8 * 7 + 8 + 8 * 2 + 8 * 2 + 8 + 8 + 8 * 2
     assert ctypes.sizeof(N.DecodeShape) == 4 * 4 + 8 * 2 + 8
-    # ia_block_summaries: 4 pointers, 3 int32 (+pad), 3 pointers, 2 int32
-    assert ctypes.sizeof(N.BlockSummaries) == 8 * 4 + 4 * 4 + 8 * 3 + 4 * 2
+    # ia_block_summaries: 4 pointers, 3 int32 (+pad), 3 pointers, 3 int32 (+pad)
+    assert ctypes.sizeof(N.BlockSummaries) == 8 * 4 + 4 * 4 + 8 * 3 + 4 * 4
     # ia_suffix_kv: 2 pointers, 6 int64, pointer, 2 int32
     assert ctypes.sizeof(N.SuffixKV) == 8 * 2 + 8 * 6 + 8 + 4 * 2
     # ia_block_keys: 2 int32, 3 pointers, 2 int64

@@ -549,7 +549,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if w.get("mode") == "cond":
-        line = run_condition(args, w, dev, with_dense=not args.no_dense, with_cpu=not args.no_cpu_baseline)
+        line = run_condition(args, w, dev, with_dense=not args.no_dense, with_cpu=not args.no_cpu_baseline,
+                             name=args.workload)
         print(json.dumps(line), flush=True)
         return
     name = args.workload
@@ -559,7 +560,7 @@ def main():
     extra = {}
     for other in [x for x in args.extra.split(",") if x and x != name]:
         if WORKLOADS[other].get("mode") == "cond":
-            c = run_condition(args, dict(WORKLOADS[other]), dev, with_dense=not args.no_dense,
+            c = run_condition(args, dict(WORKLOADS[other]), dev, name=other, with_dense=not args.no_dense,
                               with_cpu=not args.no_cpu_baseline)
             extra[other] = {k: c[k] for k in ("config", "value", "unit", "vs_baseline", "baseline_note", "timing",
                                               "achieved_GBps", "pct_hbm_peak", "fixed_mask", "dense_and_io_model",
@@ -683,7 +684,7 @@ def io_model(sel, counts, p, s):
     return full / sparse
 
 
-def run_condition(args, w, dev, with_dense, with_cpu):
+def run_condition(args, w, dev, with_dense, with_cpu, name=None):
     """One decode-attention layer call of the reference's condition path
     (``_condition_block_decode_output`` with the fused HIP finalize), batch 1; returns
     the JSON line."""
@@ -802,6 +803,12 @@ def run_condition(args, w, dev, with_dense, with_cpu):
                                                                                zip(layers, fixed_ws)]),
                                 replays, nl, stream)
     fixed_us = spread(fixed_per)["median_us"]
+    # which implementation the reference-API mirror took: the one-launch calls leave
+    # their scratch in the workspace
+    def one_launch(ws):
+        return any(isinstance(k, tuple) and k[:1] == ("condition_fused_scratch",) for k in ws)
+    eps_one = one_launch(layers[0]["ws"])
+    fixed_one = one_launch(fixed_ws[0])
 
     dense_us = None
     dense = None
@@ -870,9 +877,15 @@ def run_condition(args, w, dev, with_dense, with_cpu):
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "algorithmic_bytes": {"total": total, "q_out": qo_b, "summaries": summ_b, "representatives": rep_b,
                               "selected_kv_and_suffix": kv_b},
-        "roofline": {"bound": "hbm", "kernel": "whole layer call (stats, route, finalize, merge)",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("ia_condition_decode_fused (one launch: statistics, hand-off, routing, "
+                                "representatives, selected pages, merge)") if eps_one else
+                               "statistics, route, finalize and merge launches",
                      "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic_of(name)[0] if name and eps_one else None,
+                     "traffic_source": traffic_of(name)[1] if name and eps_one else None,
+                     **(kernel_avg_of(name, total) if name and eps_one else {})},
         "dense_us": None if dense_us is None else round(dense_us, 2),
         "dense_GBps": None if dense_us is None else round(dense_bytes / (dense_us * 1e-6) / 1e9, 1),
         "sparse_vs_dense_speedup": None if dense_us is None else round(dense_us / us, 2),
@@ -881,8 +894,11 @@ def run_condition(args, w, dev, with_dense, with_cpu):
                        "launch": "hipgraph" if fixed_ok else "eager",
                        "published_us": w["published_fixed_us"],
                        "vs_published": round(fixed_us / w["published_fixed_us"], 4),
-                       "note": "fixed_mask_hybrid_attention with this call's selection as the mask (route, "
-                               "finalize, merge; the reference's 'fixed real mask' run)"},
+                       "note": "fixed_mask_hybrid_attention with this call's selection as the mask (the "
+                               "reference's 'fixed real mask' run): " +
+                               ("one launch, ia_fixed_mask_decode_fused" if fixed_one else
+                                "route, finalize and merge launches"),
+                       "traffic": traffic_of(f"{name}_fixed")[0] if name and fixed_one else None},
         "cpu_baseline": cpu,
         "wall_s": round(wall, 3),
     }

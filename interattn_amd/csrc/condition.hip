@@ -875,8 +875,11 @@ int cond_fused_items(int batch, int hkv, int g, int d, int nb, int block_size, i
                               kMaxUnitsPerItem - sfx_units});
   if (m_cap < 1) return 0;
   const int64_t n_min = (nb + m_cap - 1) / m_cap;
-  // about one resident round, items of at least 16 blocks where the row allows
-  int64_t n = std::min<int64_t>({resident / rows, (int64_t)kMaxItemsPerBh, std::max<int64_t>(n_min, (nb + 15) / 16),
+  // about one resident round, items of at least 32 blocks where the row allows.
+  // Measured at batch 1 x 8 kv heads (graph replays, one box): 32K (512 blocks) 16
+  // items 19.4 us against 20.3 with 32 and 21.1 with 12; 64K 16 items 21.5, 32 items
+  // 21.7; 128K 32 items 22.9 against 24.7-26.4 with 20-28.
+  int64_t n = std::min<int64_t>({resident / rows, (int64_t)kMaxItemsPerBh, std::max<int64_t>(n_min, (nb + 31) / 32),
                                  (int64_t)nb});
   if (n < n_min || n < 1 || rows * n > resident) return 0;
   return (int)n;

@@ -57,8 +57,8 @@ int check_kv(const ia_paged_kv* kv, int d) {
   if (kv->seq_scale) {
     if (kv->dtype != IA_FP8_E4M3) return fail(IA_ERR_INVALID, "seq_scale is for fp8 kv only");
     if (kv->seq_scale_b_stride < 0 || kv->seq_scale_h_stride < 0 ||
-        (reinterpret_cast<uintptr_t>(kv->seq_scale) | (uintptr_t)kv->seq_scale_b_stride |
-         (uintptr_t)kv->seq_scale_h_stride) % 2 != 0)
+        reinterpret_cast<uintptr_t>(kv->seq_scale) % 8 != 0 ||
+        ((uintptr_t)kv->seq_scale_b_stride | (uintptr_t)kv->seq_scale_h_stride) % 2 != 0)
       return fail(IA_ERR_INVALID, "seq_scale pairs must be 8-byte aligned with non-negative even strides");
   }
   if (kv->block_table && (kv->bt_stride <= 0 || kv->bt_cols < 0 || kv->bt_cols > kv->bt_stride))

@@ -3,7 +3,8 @@
 // statistics, routing with representatives, selected pages and suffix, merge).
 //
 // A row (sequence, kv head) has n items (workgroups, all resident at once); item i
-// owns the row's blocks [i nb / n, (i+1) nb / n) and
+// owns the row's blocks i, i + n, i + 2 n, ... (strided, so a run of neighbouring
+// selected blocks spreads over the items instead of landing on one) and
 //   1. computes s and delta of its blocks (CBT/core.py:747-814) into LDS and its
 //      partials of the row statistics: per query row the max and sum exp of z and
 //      of zc = z + log cosh(delta) over its blocks;
@@ -31,7 +32,7 @@ struct CondLds {
   float dl[G][kCondItemBlocks];      // delta per (query row, own block)
   float lc[kCondItemBlocks];         // log(valid tokens) per own block, -inf for an empty one
   float part[kMaxItemsPerBh][4][G];  // the row's items' partials (z_m, z_l, c_m, c_l) per query row
-  float own[4][G];                   // a range's partials, as computed by the waves
+  float own[4][G];                   // an item's partials, as computed by the waves
   float glob[4][G];                  // the row's globals
   float rep_acc[kFinWaves][G * D];   // representative partial per wave: sum of weight x v_bar
   float rep_m[G];                    //   its largest logit (log2 domain)
@@ -41,15 +42,16 @@ struct CondLds {
   u32 missing;
 };
 
-// 32-block steps of summary rows in flight per wave, and whether the range's first
+// 32-block steps of summary rows in flight per wave, and whether the item's first
 // v_bar rows are loaded at the start (G = 8 has no registers to spare for either)
 template <int G>
 constexpr int cond_stat_steps() { return G <= 4 ? 2 : 1; }
 template <int G>
 constexpr bool cond_vbar_early() { return G <= 4; }
 
-// First block of item i of n over a row of nb blocks.
-__device__ __forceinline__ int cond_range_lo(int i, int nb, int n) { return (int)(((int64_t)i * nb) / n); }
+// Blocks of item i of n over a row of nb blocks (i < n <= nb): i, i + n, ..., so its
+// local block j is row block i + j n.
+__device__ __forceinline__ int cond_item_blocks(int i, int nb, int n) { return (nb - i + n - 1) / n; }
 
 // Values per lane of the statistics' row reduce-scatter: s, A and B for G query rows
 // (external-mask mode: s only), padded to a power of two.
@@ -65,7 +67,7 @@ constexpr int cond_nv() {
 // mask [batch, Hkv, nb], there are no statistics to exchange, and a representative's
 // logit is bf16(q) . bf16(k_bar) / sqrt(D) + log(count) for bf16 caches (q . k_bar /
 // sqrt(D) + log(count) for fp32 caches), weighted against the largest of the item's
-// representative logits.  Returns the number of selected blocks in the item's range (their
+// representative logits.  Returns the number of selected blocks among the item's blocks (their
 // list entries in L.list); the representative partial is left in L.rep_acc (one
 // accumulator per wave, summed by the finalize's fold) / rep_m / rep_l.  Every
 // thread of the workgroup calls it.
@@ -82,16 +84,15 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   const int nb = p.nb_max;
   const int bh = b * p.n_kv_heads + h;
   const int64_t vrow = (int64_t)bh * nb;  // summary row of block 0 of this (b, h)
-  const int lo = cond_range_lo(item, nb, n_it), hi = cond_range_lo(item + 1, nb, n_it);
-  const int m = hi - lo;  // >= 1: the host keeps n_it <= nb
+  const int m = cond_item_blocks(item, nb, n_it);  // >= 1: the host keeps n_it <= nb
   const bool kbf = SBF || p.c_kbar_bf16, xbf = SBF || p.c_bounds_bf16, vbf = SBF || p.c_vbar_bf16;
 
   constexpr int kSteps = cond_stat_steps<G>();
   constexpr bool kEarlyV = cond_vbar_early<G>();
   // ---- issued first: the query rows for the statistics (row g at the lane's dims
-  // c16 DPL ..), this thread's block (t <-> lo + t): its count and norm bound, and
-  // (G <= 4) the v_bar rows of the range's first two 32-block steps (every row index
-  // clamped into the range, so no load sits under a per-lane branch).  The query is
+  // c16 DPL ..), this thread's block (local t <-> item + t n_it): its count and norm
+  // bound, and (G <= 4) the v_bar rows of the item's first two 32-block steps (every
+  // local index clamped below m, so no load sits under a per-lane branch).  The query is
   // kept as raw words on both dtypes and converted after the summaries' loads are
   // issued: a conversion under a dtype branch would wait for the query first.
   SumRow<DPL> qw[G];
@@ -100,7 +101,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   for (int g = 0; g < G; ++g)
     qw[g].load(p.q, (int64_t)b * p.q_batch_stride + (int64_t)(h * G + g) * p.q_row_stride + c16 * DPL, qbf);
   const bool mine = t < m;
-  const int jt = lo + min(t, m - 1);
+  const int jt = item + min(t, m - 1) * n_it;
   const int cnt_ld = p.c_counts[(int64_t)b * nb + jt];
   const float bc_ld = MASK ? 0.f : p.c_vnorm_max[vrow + jt];
   const float b_all = MASK ? 0.f : p.c_vnorm_all[bh];
@@ -109,25 +110,25 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   if constexpr (kEarlyV) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      vpre[u].load(p.c_vbar, (vrow + lo + min(32 * u + 4 * wave + r, m - 1)) * D + c16 * DPL, vbf);
+      vpre[u].load(p.c_vbar, (vrow + item + min(32 * u + 4 * wave + r, m - 1) * n_it) * D + c16 * DPL, vbf);
   }
 
-  // ---- step 1: s and delta of blocks [rlo, rhi) into L.s / L.dl, log(count) into
-  // L.lc: block rlo + 32 step + 4 w + r on the 16 lanes of row r of wave w.  With
+  // ---- step 1: s and delta of item ri's blocks into L.s / L.dl, log(count) into
+  // L.lc: its local block 32 step + 4 w + r on the 16 lanes of row r of wave w.  With
   // A = sum q (k_max + k_min) and B = sum |q| (k_max - k_min) (upper/lower = (A +- B)/2):
   // s = q.k_bar / sqrt(D), delta = |A/2 - s| + B/2 (in units of 1/sqrt(D)).  Each lane's
   // 3 G partial sums are reduce-scattered over its 16-lane row; lane c16 = g then
   // gathers s, A and B of query row g.
-  auto stats_range = [&](int rlo, int rhi) {
-    const int rm = rhi - rlo;
+  auto item_stats = [&](int ri) {
+    const int rm = cond_item_blocks(ri, nb, n_it);
     const int nsteps = (rm + 31) / 32;
-    const int cl = t < rm ? p.c_counts[(int64_t)b * nb + rlo + t] : 0;
+    const int cl = t < rm ? p.c_counts[(int64_t)b * nb + ri + t * n_it] : 0;
     for (int s0 = 0; s0 < nsteps; s0 += kSteps) {
       SumRow<DPL, SBF> kb[kSteps];
       BoundRows<DPL, SBF> kx[MASK ? 1 : kSteps];
 #pragma unroll
       for (int u = 0; u < kSteps; ++u) {
-        const int64_t off = (vrow + rlo + min(32 * (s0 + u) + 4 * wave + r, rm - 1)) * D + c16 * DPL;
+        const int64_t off = (vrow + ri + min(32 * (s0 + u) + 4 * wave + r, rm - 1) * n_it) * D + c16 * DPL;
         kb[u].load(p.c_kbar, off, kbf);
         if constexpr (!MASK) {
           kx[u].load(p.c_kmax, p.c_kmin, off, xbf, p.c_bounds_packed);
@@ -205,13 +206,13 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     }
   };
 
-  // the partials of the range whose s, delta and log(count) are in L.s / L.dl / L.lc
+  // the partials of the item whose s, delta and log(count) are in L.s / L.dl / L.lc
   // (rm blocks): per query row the max and sum exp of z = s + log(count) and of zc.
   // Wave w takes (value, row) pairs w, w + 8, ...: each lane an online (max, sum) over
   // blocks lane, lane + 64, ..., then one (max, sum) reduction over the wave.  The
-  // same code for any range, so a partial recomputed by another item has the same bits.
+  // same code for any item, so a partial recomputed by another item has the same bits.
   // Leaves the partials in L.own (readable after its final barrier).
-  auto range_partial = [&](int rm) {
+  auto item_partial = [&](int rm) {
     for (int pr = wave; pr < 2 * G; pr += kFinWaves) {
       const int wh = pr / G, g = pr - wh * G;
       float mx = kNegInf, sm = 0.f;
@@ -239,9 +240,9 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     __syncthreads();
   };
 
-  stats_range(lo, hi);
+  item_stats(item);
   __syncthreads();
-  if constexpr (!MASK) range_partial(m);
+  if constexpr (!MASK) item_partial(m);
   if (MASK) {
   } else if (n_it > 1) {  // (a row of one item hands nothing over: every published word
                    // belongs to a call that advances the row's epoch)
@@ -270,18 +271,17 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     }
     if (miss) L.missing = 1u;
     __syncthreads();
-    if (L.missing) {  // a partner's partial missed the bound: every other range here
+    if (L.missing) {  // a partner's partial missed the bound: every other item's here
       if (t == 0) note_wait_fallback();
       for (int i = 0; i < n_it; ++i) {
         if (i == item) continue;
-        const int ilo = cond_range_lo(i, nb, n_it), ihi = cond_range_lo(i + 1, nb, n_it);
-        stats_range(ilo, ihi);
+        item_stats(i);
         __syncthreads();
-        range_partial(ihi - ilo);
+        item_partial(cond_item_blocks(i, nb, n_it));
         if (t < 4 * G) L.part[i][t / G][t % G] = L.own[t / G][t % G];
         __syncthreads();
       }
-      stats_range(lo, hi);  // the own range's s and delta again, for the routing
+      item_stats(item);  // the own blocks' s and delta again, for the routing
       __syncthreads();
     }
   } else if (t < 4 * G) {
@@ -341,7 +341,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
   if (!MASK && p.c_selected && mine) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
-      p.c_selected[((int64_t)b * p.n_kv_heads * G + h * G + g) * nb + lo + t] = sel ? 1 : 0;
+      p.c_selected[((int64_t)b * p.n_kv_heads * G + h * G + g) * nb + jt] = sel ? 1 : 0;
   }
   const unsigned long long bal = __ballot(sel);
   if (lane == 0) L.wcnt[wave] = __popcll(bal);
@@ -358,7 +358,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     off += w < wave ? L.wcnt[w] : 0;
     n_sel += L.wcnt[w];
   }
-  if (sel) L.list[off + __popcll(bal & ((1ull << lane) - 1ull))] = list_entry(lo + t, cnt);
+  if (sel) L.list[off + __popcll(bal & ((1ull << lane) - 1ull))] = list_entry(jt, cnt);
   // the weights' sum per query row: wave g (in-lane sums, then one wave sum)
   if (wave < G) {
     float ls = 0.f;
@@ -370,7 +370,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
       L.rep_m[wave] = (ls == 0.f || L.glob[0][wave] == kNegInf) ? kNegInf : L.glob[0][wave] * kLog2e;
     }
   }
-  // weighted v_bar: block lo + 32 step + 4 w + r on the 16 lanes of row r of wave w,
+  // weighted v_bar: local block 32 step + 4 w + r on the 16 lanes of row r of wave w,
   // weight and value rounded to bf16 for bf16 caches
   float acc[G][DPL];
 #pragma unroll
@@ -386,7 +386,7 @@ __device__ __forceinline__ int cond_fused_prologue_t(const DecodeParams& p, Cond
     } else {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        vr[u].load(p.c_vbar, (vrow + lo + min(32 * (s0 + u) + 4 * wave + r, m - 1)) * D + c16 * DPL, vbf);
+        vr[u].load(p.c_vbar, (vrow + item + min(32 * (s0 + u) + 4 * wave + r, m - 1) * n_it) * D + c16 * DPL, vbf);
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {

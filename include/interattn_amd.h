@@ -325,9 +325,9 @@ IA_API int ia_condition_decode(const ia_decode_shape* shape, const void* q,
                                void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * ia_condition_decode in one launch.  Each (sequence, kv head) row is split into
- * items that own equal runs of its blocks; an item computes the statistics of its
- * blocks, the row's items exchange their partials of the row statistics (tagged
+ * ia_condition_decode in one launch.  Each (sequence, kv head) row is split into n
+ * items, item i owning blocks i, i + n, i + 2n, ... (so neighbouring selected blocks
+ * spread over the items); an item computes the statistics of its blocks, the row's items exchange their partials of the row statistics (tagged
  * words in the workspace, each wait bounded by the wait limit, a partial still
  * missing then computed by the waiting item itself), every item merges them in
  * item order, routes its blocks, forms the representative partial of its

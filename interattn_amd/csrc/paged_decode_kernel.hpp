@@ -735,6 +735,10 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // bf16 / fp8 caches: Q.K and P.V on MFMA (query rows padded to the 16-row tile)
   constexpr bool kMfma = kDot2;
   constexpr int kMfmaK = D / 32;  // 32-dim k-slices of Q.K
+  // fp32 caches with G x D / 16 > 32 query words per lane (G = 8 at D = 128): the
+  // query rows are read from LDS inside the subtile loop instead of being held in
+  // registers, which keeps the instance within 256 registers (no spill)
+  constexpr bool kQLds = !kDot2 && G * DPL > 32;
 
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
@@ -749,6 +753,7 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ int fsel[SRC == kSrcTopkFused ? kMaxUnitsPerItem : 1];
   __shared__ TopkLds<kFinThreads> ftk;
   __shared__ float wacc_lds[kFinWaves][G * D];
+  __shared__ float q_lds[kQLds ? G * D : 1];
   __shared__ float wm_lds[kFinWaves][G];
   __shared__ float wl_lds[kFinWaves][G];
 
@@ -1523,6 +1528,16 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     }
 
+    if constexpr (kQLds) {
+      if (wave == 0 && r == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) q_lds[g * D + c16 * DPL + e] = __uint_as_float(qw[g][e]);
+      }
+      __syncthreads();
+    }
+
     // Per-lane ownership of reduce-scattered scores: token step and query rows.
     const int my_step = c16 >> 2;
     int my_g[KG];
@@ -1601,12 +1616,27 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
               a = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(qw[g][w]), as_bf16x2(kx[i][w]), a, false);
             part[i * G + g] = a;
           }
-        } else {
+        } else if constexpr (!kQLds) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             float a = 0.f;
 #pragma unroll
             for (int e = 0; e < DPL; ++e) a = fmaf(__uint_as_float(qw[g][e]), __uint_as_float(kb[i][e]), a);
+            part[i * G + g] = a;
+          }
+        }
+      }
+      if constexpr (kQLds) {  // the same dot products, query row g read once per subtile
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float qg[DPL];
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) qg[e] = q_lds[g * D + c16 * DPL + e];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float a = 0.f;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) a = fmaf(qg[e], __uint_as_float(kb[i][e]), a);
             part[i * G + g] = a;
           }
         }

@@ -37,6 +37,7 @@ CASES = [
     ("block256", 1, 8, 2, 128, [2000], 16, 256, "bf16", (2, 0, 1, False), False),
     ("c4_small", 2, 32, 8, 128, [8192, 6000], 16, 128, "bf16", (16, 0, 0, False), False),
     ("f32_d128", 2, 8, 2, 128, [700, 333], 32, 32, "f32", (4, 1, 1, False), False),
+    ("f32_g8_d128", 2, 16, 2, 128, [900, 517], 16, 32, "f32", (5, 1, 1, False), False),
 ]
 IDS = [c[0] for c in CASES]
 

@@ -106,11 +106,15 @@ struct BoundRows {
     a.load(kmax, pk ? 2 * off : off, bf16);
     b.load(pk ? kmax : kmin, pk ? 2 * off + DPL : off, bf16);
   }
+  // (each branch indexes within its row for the e it serves: no out-of-range index,
+  // not even an unused one, so the rows stay in registers)
   __device__ __forceinline__ float mx(int e, bool bf16) const {
-    return packed ? (e < DPL / 2 ? a.at(2 * e, bf16) : b.at(2 * e - DPL, bf16)) : a.at(e, bf16);
+    if (e < DPL / 2) return packed ? a.at(2 * e, bf16) : a.at(e, bf16);
+    return packed ? b.at(2 * e - DPL, bf16) : a.at(e, bf16);
   }
   __device__ __forceinline__ float mn(int e, bool bf16) const {
-    return packed ? (e < DPL / 2 ? a.at(2 * e + 1, bf16) : b.at(2 * e + 1 - DPL, bf16)) : b.at(e, bf16);
+    if (e < DPL / 2) return packed ? a.at(2 * e + 1, bf16) : b.at(e, bf16);
+    return packed ? b.at(2 * e + 1 - DPL, bf16) : b.at(e, bf16);
   }
 };
 

@@ -122,9 +122,18 @@ struct RawBounds {
     b.zero();
     packed = false;
   }
-  __device__ __forceinline__ float mx(int e) const { return packed ? (e < DPL / 2 ? a[2 * e] : b[2 * e - DPL]) : a[e]; }
+  // (both candidates are read first and passed through an empty asm, so the choice
+  // is between two values: a choice between two elements of one row would be turned
+  // into a row index chosen at run time, which puts the rows in scratch memory)
+  __device__ __forceinline__ static float pick(bool pk, float x, float y) {
+    asm("" : "+v"(x), "+v"(y));
+    return pk ? x : y;
+  }
+  __device__ __forceinline__ float mx(int e) const {
+    return e < DPL / 2 ? pick(packed, a[2 * e], a[e]) : pick(packed, b[2 * e - DPL], a[e]);
+  }
   __device__ __forceinline__ float mn(int e) const {
-    return packed ? (e < DPL / 2 ? a[2 * e + 1] : b[2 * e + 1 - DPL]) : b[e];
+    return e < DPL / 2 ? pick(packed, a[2 * e + 1], b[e]) : pick(packed, b[2 * e + 1 - DPL], b[e]);
   }
 };
 

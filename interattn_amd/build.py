@@ -6,6 +6,7 @@ The library exports only the C ABI declared in ``include/interattn_amd.h``.
 """
 
 import concurrent.futures
+import json
 import os
 import shutil
 import subprocess
@@ -29,7 +30,30 @@ FLAGS = [
     # keep packed fp32 (v_pk_*_f32) out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"),
+    # per-kernel register, scratch and occupancy report, kept in _build/kernel_resources.json
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+RESOURCES = os.path.join(BUILD, "kernel_resources.json")
+
+
+def _resources(stderr, src):
+    """Per-kernel figures from the kernel-resource-usage remarks of one compile."""
+    out, name = {}, None
+    for line in stderr.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        body = body.split(" [-Rpass-analysis")[0]
+        if body.startswith("Function Name:"):
+            name = body.split(":", 1)[1].strip()
+            out.setdefault(name, {"source": os.path.basename(src)})
+        elif name is not None and ":" in body:
+            key, val = body.rsplit(":", 1)
+            key = {"VGPRs": "vgprs", "AGPRs": "agprs", "ScratchSize [bytes/lane]": "scratch_bytes",
+                   "Occupancy [waves/SIMD]": "occupancy", "LDS Size [bytes/block]": "lds_bytes"}.get(key.strip())
+            if key and val.strip().isdigit():
+                out[name][key] = int(val.strip())
+    return out
 
 
 def _compile(src):
@@ -37,10 +61,10 @@ def _compile(src):
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     t0 = time.time()
     res = subprocess.run(cmd, capture_output=True, text=True)
-    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l and "remark:" not in l)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{err}")
-    return obj, time.time() - t0
+    return obj, time.time() - t0, _resources(res.stderr, src)
 
 
 def build(verbose=True):
@@ -49,11 +73,18 @@ def build(verbose=True):
     jobs = min(len(srcs), max(1, (os.cpu_count() or 2)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
         results = list(ex.map(_compile, srcs))
-    for obj, dt in results:
+    resources = {}
+    for obj, dt, res in results:
+        resources.update(res)
         if verbose:
             print(f"[build] {os.path.basename(obj)} {dt:.1f}s", flush=True)
+    with open(RESOURCES, "w") as f:
+        json.dump(resources, f, indent=1, sort_keys=True)
+    for name, r in sorted(resources.items()):
+        if r.get("scratch_bytes", 0) > 0:
+            print(f"[build] warning: {name} uses {r['scratch_bytes']} bytes of scratch per lane", flush=True)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for o, _ in results]]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *[o for o, _, _ in results]]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stderr)

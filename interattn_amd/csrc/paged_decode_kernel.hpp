@@ -1320,32 +1320,44 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       issue(ring[k], kbuf[k], vbuf[k], xbuf[k]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    bool done = false;
+    // The wave's subtiles (k = wave, wave + 8, ... < n_sub) in whole rotations of the
+    // ring, then the remainder: the loop has one exit, at its latch.  (An exit from
+    // the middle of a rotation would reach the loop head through a flag, and the
+    // compiler's wait counts there, merged over both edges, drained the loads in
+    // flight once per rotation.)
+    static_assert(NBUF >= 2 && NBUF <= 4, "ring of 2 to 4 buffers");
     int n_done = 0;
-    while (!done) {
-#pragma unroll
-      for (int k = 0; k < NBUF; ++k) {
-        const int fk = (k + NBUF - 1) % NBUF;  // free buffer
-        const int pk = (k + NBUF - 2) % NBUF;  // most recently issued
-        if (ring[k].k >= n_sub) {
-          done = true;
-          break;
-        }
-        ring[fk] = next(ring[pk]);
-        issue(ring[fk], kbuf[fk], vbuf[fk], xbuf[fk]);
-        __builtin_amdgcn_sched_barrier(0);
-        consume(ring[k], kbuf[k], vbuf[k], xbuf[k]);
-        // the two waves of a SIMD (w, w ^ 4) stream equal shares, but issue
-        // arbitration favours the older one; the wave ahead yields priority so
-        // both finish together (the assignment, hence the result, is unchanged)
-        ++n_done;
-        wprog[wave] = n_done;
-        const int other = wprog[wave ^ (kFinWaves / 2)];
-        if (n_done > other) __builtin_amdgcn_s_setprio(0);
-        else if (n_done < other) __builtin_amdgcn_s_setprio(2);
-        else __builtin_amdgcn_s_setprio(1);
-      }
+    auto step = [&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      constexpr int fk = (k + NBUF - 1) % NBUF;  // free buffer
+      constexpr int pk = (k + NBUF - 2) % NBUF;  // most recently issued
+      ring[fk] = next(ring[pk]);
+      issue(ring[fk], kbuf[fk], vbuf[fk], xbuf[fk]);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(ring[k], kbuf[k], vbuf[k], xbuf[k]);
+      // the two waves of a SIMD (w, w ^ 4) stream equal shares, but issue
+      // arbitration favours the older one; the wave ahead yields priority so
+      // both finish together (the assignment, hence the result, is unchanged)
+      ++n_done;
+      wprog[wave] = n_done;
+      const int other = wprog[wave ^ (kFinWaves / 2)];
+      if (n_done > other) __builtin_amdgcn_s_setprio(0);
+      else if (n_done < other) __builtin_amdgcn_s_setprio(2);
+      else __builtin_amdgcn_s_setprio(1);
+    };
+    const int n_my = wave < n_sub ? (n_sub - wave + kFinWaves - 1) / kFinWaves : 0;
+    const int n_rot = n_my / NBUF, rem = n_my - n_rot * NBUF;
+    for (int rot = 0; rot < n_rot; ++rot) {
+      step(std::integral_constant<int, 0>{});
+      step(std::integral_constant<int, 1>{});
+      if constexpr (NBUF > 2) step(std::integral_constant<int, 2>{});
+      if constexpr (NBUF > 3) step(std::integral_constant<int, 3>{});
     }
+    if (rem > 0) step(std::integral_constant<int, 0>{});
+    if constexpr (NBUF > 2)
+      if (rem > 1) step(std::integral_constant<int, 1>{});
+    if constexpr (NBUF > 3)
+      if (rem > 2) step(std::integral_constant<int, 2>{});
   };
 
   if constexpr (kMfma) {

@@ -565,42 +565,38 @@ __device__ __forceinline__ void merge_combine(int ng, GM gm, GL gl, GA ga, Store
 // arithmetic, so the output equals the two-step path's bit for bit (which lane
 // computes an output does not change its arithmetic).  The row's partials sit in
 // the slots of its workgroups, slot0 .. slot0 + n - 1.  Each thread merges outputs
-// o = threadIdx.x + kFinThreads k; the first pass's slot loads are issued together
-// with the (m, l) loads that are staged in LDS, so the merge costs one round trip.
-template <int D, int G>
+// o = threadIdx.x + kFinThreads k.  NGL = the merge groups loaded (a power of two
+// >= ceil(n / 8), chosen by the caller): every load is unconditional (slot indices
+// clamped; slots past n are weighed by 0), the (m, l) words first and the first
+// pass's accumulators after them, so the wait for the (m, l) words leaves the
+// accumulators in flight and the merge of up to 32 slots costs one round trip
+// (more slots: a second batch of four groups after the first).  (Loads under
+// per-group branches made the compiler wait for half of them at a branch join
+// before the (m, l) loads went out: two round trips.)
+template <int D, int G, int NGL>
 __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h, int64_t slot0, int n) {
+  static_assert(NGL >= 1 && NGL <= kMergeGroups, "merge groups");
   constexpr int NO = (G * D + kFinThreads - 1) / kFinThreads;  // outputs per thread
+  constexpr int NB = NGL < 4 ? NGL : 4;                        // groups per load batch
+  constexpr int NBATCH = NGL / NB;
   __shared__ float ml_lds[kMaxItemsPerBh][G][2];
-  float acc[kMergeGroups][kMergeGroup];
-  const int ng_load = (n + kMergeGroup - 1) / kMergeGroup;
-  // one uniform branch per group of 8 slots, its loads issued back to back (slots past
-  // n re-read slot n - 1: the merge weighs them by 0)
-  auto load_acc = [&](int o) {
-#pragma unroll
-    for (int g = 0; g < kMergeGroups; ++g) {
-      if (g < ng_load) {
-#pragma unroll
-        for (int j = 0; j < kMergeGroup; ++j) {
-          const int s = min(kMergeGroup * g + j, n - 1);
-          acc[g][j] = ld_agent(p.part_acc + (slot0 + s) * (G * D) + o);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < kMergeGroup; ++j) acc[g][j] = 0.f;
-      }
-    }
-  };
-  if (threadIdx.x < G * D) load_acc(threadIdx.x);
   constexpr int kMlPer = (kMaxItemsPerBh * G + kFinThreads - 1) / kFinThreads;
   float mlv[kMlPer][2];
 #pragma unroll
   for (int i = 0; i < kMlPer; ++i) {
-    const int t = threadIdx.x + kFinThreads * i;
-    if (t < n * G) {
-      mlv[i][0] = ld_agent(p.part_ml + (slot0 * G + t) * 2);
-      mlv[i][1] = ld_agent(p.part_ml + (slot0 * G + t) * 2 + 1);
-    }
+    const int t = min(threadIdx.x + kFinThreads * i, n * G - 1);
+    mlv[i][0] = ld_agent(p.part_ml + (slot0 * G + t) * 2);
+    mlv[i][1] = ld_agent(p.part_ml + (slot0 * G + t) * 2 + 1);
   }
+  float acc[NB][kMergeGroup];
+  auto load_acc = [&](int o, int gb) {  // groups gb .. gb + NB - 1
+#pragma unroll
+    for (int g = 0; g < NB; ++g)
+#pragma unroll
+      for (int j = 0; j < kMergeGroup; ++j)
+        acc[g][j] = ld_agent(p.part_acc + (slot0 + min(kMergeGroup * (gb + g) + j, n - 1)) * (G * D) + o);
+  };
+  load_acc(threadIdx.x < G * D ? threadIdx.x : 0, 0);
 #pragma unroll
   for (int i = 0; i < kMlPer; ++i) {
     const int t = threadIdx.x + kFinThreads * i;
@@ -616,7 +612,6 @@ __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h,
   for (int k = 0; k < NO; ++k) {
     const int o = threadIdx.x + kFinThreads * k;
     if (o >= G * D) break;
-    if (k > 0) load_acc(o);
     const int g0 = o / D;
     float gM[kMergeGroups], gL[kMergeGroups], ga[kMergeGroups][1];
 #pragma unroll
@@ -624,16 +619,24 @@ __device__ __forceinline__ void fused_merge(const DecodeParams& p, int b, int h,
       gM[g] = kNegInf;
       gL[g] = 0.f;
       ga[g][0] = 0.f;
-      if (g < ng) {
-        float mv[kMergeGroup], lv[kMergeGroup], av[kMergeGroup][1];
+    }
 #pragma unroll
-        for (int j = 0; j < kMergeGroup; ++j) {
-          const int s = kMergeGroup * g + j;
-          mv[j] = s < n ? ml_lds[s][g0][0] : kNegInf;
-          lv[j] = s < n ? ml_lds[s][g0][1] : 0.f;
-          av[j][0] = acc[g][j];
+    for (int bt = 0; bt < NBATCH; ++bt) {
+      if (k > 0 || bt > 0) load_acc(o, NB * bt);
+#pragma unroll
+      for (int gi = 0; gi < NB; ++gi) {
+        const int g = NB * bt + gi;
+        if (g < ng) {
+          float mv[kMergeGroup], lv[kMergeGroup], av[kMergeGroup][1];
+#pragma unroll
+          for (int j = 0; j < kMergeGroup; ++j) {
+            const int s = kMergeGroup * g + j;
+            mv[j] = s < n ? ml_lds[s][g0][0] : kNegInf;
+            lv[j] = s < n ? ml_lds[s][g0][1] : 0.f;
+            av[j][0] = acc[gi][j];
+          }
+          merge_group<1>(mv, lv, av, gM[g], gL[g], ga[g]);
         }
-        merge_group<1>(mv, lv, av, gM[g], gL[g], ga[g]);
       }
     }
     merge_combine<1>(
@@ -735,10 +738,10 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // bf16 / fp8 caches: Q.K and P.V on MFMA (query rows padded to the 16-row tile)
   constexpr bool kMfma = kDot2;
   constexpr int kMfmaK = D / 32;  // 32-dim k-slices of Q.K
-  // fp32 caches with G x D / 16 > 32 query words per lane (G = 8 at D = 128): the
+  // fp32 caches with G x D / 16 >= 32 query words per lane (G >= 4 at D = 128): the
   // query rows are read from LDS inside the subtile loop instead of being held in
   // registers, which keeps the instance within 256 registers (no spill)
-  constexpr bool kQLds = !kDot2 && G * DPL > 32;
+  constexpr bool kQLds = !kDot2 && G * DPL >= 32;
 
   __shared__ int unit_lo[kMaxUnitsPerItem];
   __shared__ int unit_hi[kMaxUnitsPerItem];
@@ -1841,8 +1844,12 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       if (merge_todo[0]) {
         if (n_items_row <= kMergeGroup)
           fused_merge_tagged<D, G>(p, b, h, (int64_t)fused_slot - item, n_items_row, partial_tag(bh, row_epoch));
+        else if (n_items_row <= 2 * kMergeGroup)
+          fused_merge<D, G, 2>(p, b, h, (int64_t)fused_slot - item, n_items_row);
+        else if (n_items_row <= 4 * kMergeGroup)
+          fused_merge<D, G, 4>(p, b, h, (int64_t)fused_slot - item, n_items_row);
         else
-          fused_merge<D, G>(p, b, h, (int64_t)fused_slot - item, n_items_row);
+          fused_merge<D, G, kMergeGroups>(p, b, h, (int64_t)fused_slot - item, n_items_row);
       }
     }
   }

@@ -86,6 +86,19 @@ struct KvFp8 {
   static constexpr int kRing = 3;
 };
 
+// NW words (2 or 4) at p with one plain, cached load
+template <int NW>
+__device__ __forceinline__ void load_cached_words(const char* p, u32* w) {
+  static_assert(NW == 2 || NW == 4, "8- or 16-byte pieces");
+  if constexpr (NW == 4) {
+    const u32x4_t a = *reinterpret_cast<const u32x4_t*>(p);
+    w[0] = a[0]; w[1] = a[1]; w[2] = a[2]; w[3] = a[3];
+  } else {
+    const u32x2_t a = *reinterpret_cast<const u32x2_t*>(p);
+    w[0] = a[0]; w[1] = a[1];
+  }
+}
+
 // NWD words of one K/V row slice, as streaming loads
 template <int NWD>
 __device__ __forceinline__ void load_words(const char* p, u32* w) {
@@ -783,15 +796,29 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // row c16 % G at the dims of the lane's k-slices.
   constexpr int QR0 = kMfma ? kMfmaK : G;
   constexpr int QR1 = kMfma ? 8 : DPL;
-  u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs (upper half unused)
+  u32 qraw[QR0][QR1];  // f32 q: floats; bf16 q: pairs in the lower half (upper half unused)
+  // One-launch top-k call: the same two plain loads on both q dtypes, straight into
+  // qraw, with no load under a branch and no arithmetic on the loaded words until they
+  // are used (f32 rows read their two halves, bf16 rows their one half twice, the copy
+  // landing in the unused upper half): loads under the dtype branch made the compiler
+  // wait for every load in flight before each of them, in the middle of the selection
+  // (C3 -0.5, C5 -0.4, C2 -0.2 us).  The other sources load q at the start, where the
+  // branch-free form's extra loads sit ahead of the first summary rows and measured
+  // slower (one-launch eps-rule call +0.4-0.7 us), so they keep the dtype branch.
   auto load_q = [&](int bq, int hq) {
+    const bool qf = p.q_f32 != 0;
 #pragma unroll
     for (int x = 0; x < QR0; ++x) {
       const int g = kMfma ? c16 % G : x;
       const int d0 = kMfma ? mfma_kslice<KV::kBytes>(x, r) : c16 * DPL;
       constexpr int NE = kMfma ? 8 : DPL;
+      static_assert(NE == QR1, "one query slice per row of qraw");
       const int64_t row = (int64_t)bq * p.q_batch_stride + (int64_t)(hq * G + g) * p.q_row_stride;
-      if (p.q_f32) {
+      if constexpr (SRC == kSrcTopkFused) {
+        const char* q0 = reinterpret_cast<const char*>(p.q) + (row + d0) * (qf ? 4 : 2);
+        load_cached_words<NE / 2>(q0, qraw[x]);
+        load_cached_words<NE / 2>(qf ? q0 + NE * 2 : q0, qraw[x] + NE / 2);
+      } else if (qf) {
         const u32* qp = reinterpret_cast<const u32*>(p.q) + row + d0;
 #pragma unroll
         for (int e = 0; e < NE; ++e) qraw[x][e] = qp[e];

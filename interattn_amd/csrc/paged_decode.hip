@@ -275,6 +275,10 @@ int run_topk_decode(const ia_decode_shape* shape, const void* q, const ia_paged_
   p.unit_tokens = block_size;
   p.nb_max = nb_max;
   p.k_per_seq = k_per_seq;
+  // launches with per-sequence k (variable-length batches) load keys as whole rows: the
+  // faster form where items differ in length and stream partly alone; uniform batches
+  // keep the operand-layout loads (same results either way)
+  p.key_rows = k_per_seq != nullptr;
   p.topk_k = k;
   p.forced_first = forced_first;
   p.forced_last = forced_last;

@@ -18,6 +18,12 @@ int run_bf16(const DecodeParams& p, int src, dim3 grid, hipStream_t st, int* res
       if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcLists>(), IA_OK;
       return launch_paged_finalize<D, G, KvBf16, kSrcLists>(p, grid, st);
     case kSrcTopkFused:
+      if constexpr (D == 128) {
+        if (p.key_rows) {  // keys as whole rows through LDS
+          if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcTopkFused, true>(), IA_OK;
+          return launch_paged_finalize<D, G, KvBf16, kSrcTopkFused, true>(p, grid, st);
+        }
+      }
       if (resident) return *resident = resident_wgs<D, G, KvBf16, kSrcTopkFused>(), IA_OK;
       return launch_paged_finalize<D, G, KvBf16, kSrcTopkFused>(p, grid, st);
     case kSrcCondFused:  // the one-launch condition call runs groups of up to 4 query rows

@@ -194,6 +194,7 @@ struct DecodeParams {
   int32_t kb_bf16;
   int32_t score_quest;
   float score_scale;
+  int32_t key_rows;          // one-launch top-k call: run the instance that loads keys as whole rows
   unsigned long long* sbuf;  // [rows, nb_max] published scores: tag << 32 | score bits
   unsigned long long* tpart; // [workgroups, G D + 2 G] tagged partials (acc, then (m, l)) of rows of <= 8 items
   u32* rowctr;               // [rows, kFlagStride]: finished partials (word 0), row epoch (word 1)
@@ -735,7 +736,7 @@ __device__ __forceinline__ void fused_merge_tagged(const DecodeParams& p, int b,
 
 namespace ia {
 
-template <int D, int G, typename KV, int SRC>
+template <int D, int G, typename KV, int SRC, bool KROWS = false>
 __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_finalize(DecodeParams p) {
   constexpr int DPL = D / 16;
   constexpr int NWD = DPL * KV::kBytes / 4;
@@ -769,6 +770,19 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   __shared__ int fsel[SRC == kSrcTopkFused ? kMaxUnitsPerItem : 1];
   __shared__ TopkLds<kFinThreads> ftk;
   __shared__ float wacc_lds[kFinWaves][G * D];
+  // bf16 caches at D = 128: each wave's key subtile (16 token rows of 16 16-byte
+  // pieces) on its way from whole-row loads to the MFMA operand layout (slots
+  // XOR-swizzled per row).  Whole-row loads use full cache lines per instruction (the
+  // operand layout's loads read 64 bytes of sixteen rows), which raises one CU's
+  // stream rate where HBM is not saturated: items of uneven length (ragged rows, the
+  // condition calls' few-subtile items).  Where every workgroup streams equal shares
+  // at the HBM rate the transpose costs more than it gains (C4 +0.66 us), so the
+  // one-launch top-k call takes it in its KROWS instance only (the host picks that
+  // one for launches with per-sequence k, its variable-length batches), and the dense
+  // and top-k-list sources never.
+  constexpr bool kKeyLdsAny =
+      kMfma && kBf16 && D == 128 && ((SRC == kSrcTopkFused && KROWS) || SRC == kSrcLists || SRC == kSrcCondFused);
+  __shared__ u32x4_t key_lds[kKeyLdsAny ? kFinWaves : 1][kKeyLdsAny ? 256 : 1];
   __shared__ float q_lds[kQLds ? G * D : 1];
   __shared__ float wm_lds[kFinWaves][G];
   __shared__ float wl_lds[kFinWaves][G];
@@ -1416,7 +1430,8 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     for (int n = 0; n < DPL; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     float m_run = kNegInf, l_run = 0.f;
 
-    auto issue = [&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
+    auto issue = [&](auto kl, const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) {
+      constexpr bool kKeyLds = decltype(kl)::value;
       // (the one-launch condition call streams a few subtiles per item: past its list
       // a wave issues nothing rather than the placeholder loads)
       if constexpr (SRC == kSrcCondFused)
@@ -1426,14 +1441,26 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       int64_t kts, vts;
       sub_rows(sb, kp, vp, kts, vts);
       page_scales(sb, kp, xb);
-      // K: token rho (row 0 past the valid rows), NWD 16-byte pieces at 64*pc + 16*r
-      const char* kr = kp + (int64_t)(rho < sb.nv ? rho : 0) * kts + 16 * r;
+      if constexpr (kKeyLds) {
+        // K as whole rows, like V (step i: token 4i + r, dims c16*DPL ..): each load
+        // instruction reads four full 256-byte rows, where the operand layout below
+        // would read 64 bytes of sixteen rows (half lines, which cap a CU's stream
+        // rate); consume passes them through LDS to the operand layout
 #pragma unroll
-      for (int pc = 0; pc < NWD; ++pc) {
-        const u32x4_t a = ld_stream16(kr + 64 * pc);
-        const u32 w4[4] = {a[0], a[1], a[2], a[3]};
+        for (int i = 0; i < 4; ++i) {
+          const int tl = (4 * i + r < sb.nv) ? 4 * i + r : 0;
+          load_words<NWD>(kp + (int64_t)tl * kts + lane_off, kb[i]);
+        }
+      } else {
+        // K: token rho (row 0 past the valid rows), NWD 16-byte pieces at 64*pc + 16*r
+        const char* kr = kp + (int64_t)(rho < sb.nv ? rho : 0) * kts + 16 * r;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kb[(4 * pc + e) / NWD][(4 * pc + e) % NWD] = w4[e];
+        for (int pc = 0; pc < NWD; ++pc) {
+          const u32x4_t a = ld_stream16(kr + 64 * pc);
+          const u32 w4[4] = {a[0], a[1], a[2], a[3]};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kb[(4 * pc + e) / NWD][(4 * pc + e) % NWD] = w4[e];
+        }
       }
       // V: step i, token 4i + r, dims c16*DPL ..
 #pragma unroll
@@ -1443,14 +1470,35 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     };
 
-    auto consume = [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
+    auto consume = [&](auto kl, const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
+      constexpr bool kKeyLds = decltype(kl)::value;
       auto kword = [&](int fw) -> u32 { return kb[fw / NWD][fw % NWD]; };
+      // bf16 keys through LDS: row t's 16-byte piece c at slot 16 t + (c ^ t) (the XOR
+      // spreads a column of pieces over all banks); the lane then reads piece
+      // 4 kk + r of token rho, its operand for k-slice kk (the same words the
+      // operand-layout loads gave)
+      u32x4_t kop[kKeyLds ? kMfmaK : 1];
+      if constexpr (kKeyLds) {
+        u32x4_t* kl = key_lds[wave];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 4 * i + r;
+          kl[16 * t + (c16 ^ t)] = u32x4_t{kb[i][0], kb[i][1], kb[i][2], kb[i][3]};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int kk = 0; kk < kMfmaK; ++kk) kop[kk] = kl[16 * rho + ((4 * kk + r) ^ rho)];
+        wave_lds_sync();  // (every lane's reads before the next subtile's writes)
+      }
       // ---------------- scores: token r + 4i, query row c16 % G, in accumulator i
       f32x4_t s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < kMfmaK; ++kk) {
         u32 w[4];
-        if constexpr (kFp8) {  // piece kk/2, half kk%2: 8 codes widened to bf16 (exact)
+        if constexpr (kKeyLds) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = kop[kk][e];
+        } else if constexpr (kFp8) {  // piece kk/2, half kk%2: 8 codes widened to bf16 (exact)
           const u32 c0 = kword(4 * (kk >> 1) + 2 * (kk & 1)), c1 = kword(4 * (kk >> 1) + 2 * (kk & 1) + 1);
           w[0] = fp8x2_to_bf16x2<false>(c0);
           w[1] = fp8x2_to_bf16x2<true>(c0);
@@ -1524,7 +1572,14 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       }
     };
 
-    stream(issue, consume);
+    auto run = [&](auto kl) {
+      stream([&](const Sub& sb, u32 (&kb)[4][NWD], u32 (&vb)[4][NWD], u32 (&xb)[2]) { issue(kl, sb, kb, vb, xb); },
+             [&](const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
+               consume(kl, sb, kb, vb, xb);
+             });
+    };
+    if constexpr (kKeyLdsAny) run(std::true_type{});
+    else run(std::false_type{});
 
     // ---- fold the wave: l over the four lane rows; the query rows' accumulators sit
     // in lane rows r < max(1, G/4) (row 4r + i < G)
@@ -2149,9 +2204,9 @@ __global__ __launch_bounds__(kThreads) void ia_condition_block_splitk_merge(Deco
 }
 
 // Per-instance launcher; returns IA_OK or an error code.
-template <int D, int G, typename KV, int SRC>
+template <int D, int G, typename KV, int SRC, bool KROWS = false>
 int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC>), grid, dim3(kFinThreads), 0, st, p);
+  hipLaunchKernelGGL((ia_condition_block_paged_finalize<D, G, KV, SRC, KROWS>), grid, dim3(kFinThreads), 0, st, p);
   int rc = check_launch("paged decode");
   if constexpr (src_fused(SRC)) {
     return rc;  // the row's last item merges inside the launch
@@ -2173,7 +2228,7 @@ int launch_paged_finalize(const DecodeParams& p, dim3 grid, hipStream_t st) {
 // (relaxed atomics: concurrent first calls compute the same value).  0 on a query
 // failure (the callers then assume 1024).
 constexpr int kMaxCachedDevices = 64;
-template <int D, int G, typename KV, int SRC>
+template <int D, int G, typename KV, int SRC, bool KROWS = false>
 int resident_wgs() {
   static std::atomic<int> cached[kMaxCachedDevices];
   int dev = 0;
@@ -2183,7 +2238,7 @@ int resident_wgs() {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC>), kFinThreads,
+            &per_cu, reinterpret_cast<const void*>(&ia_condition_block_paged_finalize<D, G, KV, SRC, KROWS>), kFinThreads,
             0) != hipSuccess)
       return 0;
     n = std::max(1, cus * per_cu);

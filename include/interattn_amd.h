@@ -400,7 +400,10 @@ IA_API int ia_fixed_mask_decode(const ia_decode_shape* shape, const void* q,
  * the wait limit (ia_set_wait_limit); scores still missing then are computed by
  * the waiting item itself, so the result never depends on timing.  (When every row
  * has the same work and a row has at most two items, each item scores the whole
- * row itself instead, with the same arithmetic.)  Equal to
+ * row itself instead, with the same arithmetic.  Launches with k_per_seq, the
+ * variable-length batches, load the keys as whole rows and pass them through LDS to
+ * the matrix-core operand layout, which streams faster where items differ in length;
+ * the words reaching the products are the same.)  Equal to
  * ia_select_topk + ia_sparse_paged_decode, bit for bit.  idx/n_sel (optional,
  * together) receive the selection.  Requires nb_max <= 4096 and k_cap <= 512
  * (IA_ERR_UNSUPPORTED otherwise: use the two calls).  The workspace

@@ -415,6 +415,41 @@ def test_fused_topk_decode_k_per_seq_and_fallback(device):
     assert torch.equal(out2, ref)
 
 
+@pytest.mark.parametrize("hq,hkv,page,lens", [
+    (8, 2, 16, [1, 17, 2049]),     # G = 4: a one-token sequence, a partial subtile
+    (16, 2, 32, [300, 4133, 64]),  # G = 8, two-subtile pages
+    (16, 8, 16, [999, 33, 5000]),  # G = 2
+    (8, 8, 64, [1250, 4096]),      # G = 1, pages of four subtiles
+], ids=["g4_p16", "g8_p32", "g2_p16", "g1_p64"])
+def test_key_row_instance_equals_two_step(hq, hkv, page, lens, device):
+    """Launches with per-sequence k at head_dim 128 run the instance that loads keys as
+    whole rows and passes them through LDS to the MFMA operand layout; the words that
+    reach the products are the ones the operand-layout loads give, so the output equals
+    the two-step path bit for bit, for every group size, page size and ragged length
+    (one-token sequences and partial subtiles included)."""
+    announce(f"key-row instance: G={hq // hkv} page={page} lens={lens}")
+    case = make_case(seed=31 + page + hq, batch=len(lens), hq=hq, hkv=hkv, d=128, seq_lens=lens, page_size=page)
+    dev = to_dev(case, device)
+    block = 64
+    nb_max = max(math.ceil(L / block) for L in lens)
+    kvec = torch.tensor([max(1, math.ceil(L / block) // 4) for L in lens], device=device, dtype=torch.int32)
+    k_cap = int(kvec.max()) + 2
+    summ = ia.build_block_summaries(dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], block,
+                                    nb_max=nb_max)
+    idx, n_sel = ia.select_blocks_topk(dev["q"], summ["k_bar"], dev["seq_lens"], 0, block_size=block,
+                                       k_per_seq=kvec, k_cap=k_cap, forced_first=1, forced_last=1)
+    ref = ia.sparse_paged_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"], idx,
+                                 n_sel, block_size=block)
+    ws = {}
+    for _ in range(2):  # a second call on the same workspace
+        out = ia.sparse_topk_decode(dev["q"], dev["pool_k"], dev["pool_v"], dev["block_table"], dev["seq_lens"],
+                                    summ["k_bar"], 0, block_size=block, k_per_seq=kvec, k_cap=k_cap,
+                                    forced_first=1, forced_last=1, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+    assert torch.isfinite(out.float()).all()
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_sparse_decode_with_representatives(dt, device):
     """Top-k finalize with representatives for the unselected blocks (logit

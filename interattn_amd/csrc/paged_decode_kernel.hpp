@@ -1473,21 +1473,23 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     auto consume = [&](auto kl, const Sub& sb, const u32 (&kb)[4][NWD], const u32 (&vb)[4][NWD], const u32 (&xb)[2]) {
       constexpr bool kKeyLds = decltype(kl)::value;
       auto kword = [&](int fw) -> u32 { return kb[fw / NWD][fw % NWD]; };
-      // bf16 keys through LDS: row t's 16-byte piece c at slot 16 t + (c ^ t) (the XOR
-      // spreads a column of pieces over all banks); the lane then reads piece
-      // 4 kk + r of token rho, its operand for k-slice kk (the same words the
-      // operand-layout loads gave)
+      // bf16 keys through LDS: row t's 16-byte piece c at slot 16 t + (c ^ sw(t)),
+      // sw(t) = (t >> 2) | (t & 3) << 2; the lane then reads piece 4 kk + r of token
+      // rho, its operand for k-slice kk (the same words the operand-layout loads
+      // gave).  sw(4 i + r) = i + 4 r and sw(rho) = c16, so both the writes and the
+      // reads of any 8 consecutive lanes touch 8 distinct 16-byte bank groups (with
+      // sw(t) = t the reads of lanes c16 and c16 + 2 met in one group)
       u32x4_t kop[kKeyLds ? kMfmaK : 1];
       if constexpr (kKeyLds) {
         u32x4_t* kl = key_lds[wave];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 4 * i + r;
-          kl[16 * t + (c16 ^ t)] = u32x4_t{kb[i][0], kb[i][1], kb[i][2], kb[i][3]};
+          kl[16 * t + (c16 ^ (i + 4 * r))] = u32x4_t{kb[i][0], kb[i][1], kb[i][2], kb[i][3]};
         }
         wave_lds_sync();
 #pragma unroll
-        for (int kk = 0; kk < kMfmaK; ++kk) kop[kk] = kl[16 * rho + ((4 * kk + r) ^ rho)];
+        for (int kk = 0; kk < kMfmaK; ++kk) kop[kk] = kl[16 * rho + ((4 * kk + r) ^ c16)];
         wave_lds_sync();  // (every lane's reads before the next subtile's writes)
       }
       // ---------------- scores: token r + 4i, query row c16 % G, in accumulator i

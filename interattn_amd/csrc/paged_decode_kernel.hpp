@@ -1346,7 +1346,14 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // issue: a load issued by consume would make the wave wait for every load in
   // flight (the vector memory counter drains in order).
   auto stream = [&](auto&& issue, auto&& consume) {
-    constexpr int NBUF = KV::kRing;
+    // The one-launch top-k call's long streams whose consume is the longer one (keys
+    // through LDS, fp8 codes widened) keep one subtile in flight per wave: a CU then
+    // streams faster than with two (C3 -1.0 to -1.2 us, C5 -1.2 us; same bits).  The
+    // condition-rule calls' short streams keep the deeper ring for their start.
+    constexpr int NBUF = (SRC == kSrcTopkFused && (KROWS || kFp8)) ? 2 : KV::kRing;
+    // the priority feedback below pays where the waves stream equal shares at the HBM
+    // rate, except in the uniform bf16 top-k call (C4 -0.4, C2 -0.15 us without it)
+    constexpr bool kPrioFeedback = !(SRC == kSrcTopkFused && !KROWS && kBf16);
     u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD], xbuf[NBUF][2];
     Sub ring[NBUF];
     if (n_sub == 0) return;
@@ -1383,11 +1390,13 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       // arbitration favours the older one; the wave ahead yields priority so
       // both finish together (the assignment, hence the result, is unchanged)
       ++n_done;
-      wprog[wave] = n_done;
-      const int other = wprog[wave ^ (kFinWaves / 2)];
-      if (n_done > other) __builtin_amdgcn_s_setprio(0);
-      else if (n_done < other) __builtin_amdgcn_s_setprio(2);
-      else __builtin_amdgcn_s_setprio(1);
+      if constexpr (kPrioFeedback) {
+        wprog[wave] = n_done;
+        const int other = wprog[wave ^ (kFinWaves / 2)];
+        if (n_done > other) __builtin_amdgcn_s_setprio(0);
+        else if (n_done < other) __builtin_amdgcn_s_setprio(2);
+        else __builtin_amdgcn_s_setprio(1);
+      }
     };
     const int n_my = wave < n_sub ? (n_sub - wave + kFinWaves - 1) / kFinWaves : 0;
     const int n_rot = n_my / NBUF, rem = n_my - n_rot * NBUF;

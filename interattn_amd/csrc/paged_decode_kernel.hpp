@@ -1351,9 +1351,11 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     // streams faster than with two (C3 -1.0 to -1.2 us, C5 -1.2 us; same bits).  The
     // condition-rule calls' short streams keep the deeper ring for their start.
     constexpr int NBUF = (SRC == kSrcTopkFused && (KROWS || kFp8)) ? 2 : KV::kRing;
-    // the priority feedback below pays where the waves stream equal shares at the HBM
-    // rate, except in the uniform bf16 top-k call (C4 -0.4, C2 -0.15 us without it)
-    constexpr bool kPrioFeedback = !(SRC == kSrcTopkFused && !KROWS && kBf16);
+    // the priority feedback below stays in the fp8 and key-row top-k calls (measured
+    // faster with it) and in the finalizes of the multi-launch paths; the uniform bf16
+    // top-k call (C4 -0.4, C2 -0.15 us) and the one-launch condition calls (-0.1 to
+    // -0.3 us) run without it
+    constexpr bool kPrioFeedback = !(SRC == kSrcCondFused || (SRC == kSrcTopkFused && !KROWS && kBf16));
     u32 kbuf[NBUF][4][NWD], vbuf[NBUF][4][NWD], xbuf[NBUF][2];
     Sub ring[NBUF];
     if (n_sub == 0) return;

@@ -516,7 +516,7 @@ constexpr int kMergeFastSlots = 8;  // slots per wave read in the merge's one-ro
 constexpr int kMergeGroup = kMergeFastSlots;            // slots per merge group
 constexpr int kMergeGroups = kMaxItemsPerBh / kMergeGroup;  // groups of a row's split-K items
 constexpr int kFlagStride = 64;  // u32 words between hand-off flags (one 256-byte line each)
-constexpr int kSoloItems = 2;    // fused top-k call: rows of at most this many items score the whole row per item
+constexpr int kSoloItems = 3;    // fused top-k call: rows of at most this many items score the whole row per item
 
 // The split-K merge of a row's items (balanced launches: the merge kernel and the
 // fused top-k call's in-kernel merge share it, so both give the same bits).  Slots
@@ -851,7 +851,6 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
   // (w % 8) * (grid / 8) + w / 8 puts consecutive slots -- the items of one row -- on
   // one XCD, where they share the row's block-key lines through its L2.  (Placement
   // only: any mapping gives the same results.)
-  bool rows_alike = false;  // fused top-k call: every row has the same work (uniform)
   constexpr int SDPL = D / 16;  // key dims per lane in the scorer (16 lanes per key row)
   const int fused_slot = (gridDim.x % 8 == 0)
                              ? (int)((blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8)
@@ -895,7 +894,6 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
       };
       PlanRows rows;
       const PlanRule rule = plan_rule_wave(slots_of, p.n_rows, p.plan_budget, p.max_items, nsub_u, rows);
-      rows_alike = rule.n_all > 0;
       e = plan_entry_wave(slots_of, rows, p.n_rows, rule, fused_slot, nsub_u);
       // the row's length and k from the lane that holds it
       const int row_e = __builtin_amdgcn_readfirstlane(e.row);
@@ -973,14 +971,13 @@ __global__ __launch_bounds__(kFinThreads, 2) void ia_condition_block_paged_final
     const int n_it = n_items_row;
     // (G > 4 keeps the hand-off: its query words leave no room for a second scorer form)
     constexpr bool kSoloG = G <= 4;
-    // rows of up to kSoloItems items of a launch whose rows are alike: every item
-    // scores the whole row itself (the row's items sit on one XCD and read the key
-    // lines in the same order, so the second read of a line is an L2 hit) and no
-    // scores are handed over; other rows split the scoring and hand the scores to
-    // each other.  Measured (alternating builds on one box): C5 66.4 against 67.8 us,
-    // C4 unchanged; ragged C3 rows were 0.3-0.8 us slower whole-row, so they keep the
-    // hand-off.
-    const bool solo = kSoloG && n_it <= kSoloItems && rows_alike;
+    // rows of up to kSoloItems items: every item scores the whole row itself (the
+    // row's items sit on one XCD and read the key lines in the same order, so the
+    // second read of a line is an L2 hit) and no scores are handed over; rows of more
+    // items split the scoring and hand the scores to each other.  Measured
+    // (alternating builds on one box): C5 66.4 against 67.8 us, C4 unchanged; ragged
+    // C3 rows of 1-3 items -0.4 to -0.5 us; 32-item rows (C2) +0.4 us whole-row.
+    const bool solo = kSoloG && n_it <= kSoloItems;
     auto range_lo = [&](int i) { return (i * nbs) / n_it; };  // (< 2^19: 32-bit arithmetic)
     unsigned long long* row_entries = p.sbuf + (int64_t)bh * p.nb_max;
     const int own_lo = solo ? 0 : range_lo(item), own_hi = solo ? nbs : range_lo(item + 1);
